@@ -1,0 +1,78 @@
+"""Build the gfx950 code objects and the C-ABI host library, in-tree.
+
+    python -m example_matmul_metal4_amd.build
+
+Outputs (under example_matmul_metal4_amd/lib/, git-ignored, shipped with the tree):
+  mtk_<unit>.hsaco   one code object per csrc/<unit>.hip, `hipcc --genco --offload-arch=gfx950`
+                     (replaces the reference's package.sh `xcrun metal` -> metallib step,
+                     Sources/matmul/package.sh:1-3, and its run-time makeLibrary(source:) JIT)
+  libmtk.so          host runtime (csrc/runtime.cpp) exporting include/mtk.h, linked to libamdhip64
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+import time
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "lib")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+HIP_UNITS = ["gemm_f16", "gemm_bf16", "conv", "attention", "skinny", "util"]
+
+HIPCC_FLAGS = [
+    "--genco", "--offload-arch=gfx950", "-O3", "-std=c++17",
+    # packed fp32 VALU ops stay off in every kernel (hardware issue on these boxes)
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd):
+    t0 = time.time()
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    return time.time() - t0
+
+
+def hip_unit(unit: str) -> str:
+    src = os.path.join(CSRC, unit + ".hip")
+    out = os.path.join(LIB, f"mtk_{unit}.hsaco")
+    tmp = out + ".tmp"
+    _run([os.path.join(ROCM, "bin", "hipcc")] + HIPCC_FLAGS + [src, "-o", tmp])
+    os.replace(tmp, out)
+    return out
+
+
+def host_lib() -> str:
+    out = os.path.join(LIB, "libmtk.so")
+    tmp = out + ".tmp"
+    cxx = shutil.which("g++") or "g++"
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
+          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", os.path.join(CSRC, "runtime.cpp"),
+          f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl", "-o", tmp])
+    os.replace(tmp, out)
+    return out
+
+
+def build(units=None, verbose=True) -> list[str]:
+    os.makedirs(LIB, exist_ok=True)
+    units = [u for u in (units or HIP_UNITS) if os.path.exists(os.path.join(CSRC, u + ".hip"))]
+    t0 = time.time()
+    outs = []
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(units) + 1)) as ex:
+        futs = [ex.submit(hip_unit, u) for u in units] + [ex.submit(host_lib)]
+        for f in futs:
+            outs.append(f.result())
+    if verbose:
+        print(f"[build] {len(outs)} artefacts in {time.time() - t0:.1f}s -> {LIB}", flush=True)
+    return outs
+
+
+if __name__ == "__main__":
+    build(sys.argv[1:] or None)

@@ -1,0 +1,106 @@
+// Device-side helpers shared by the gfx950 kernels: vector types, raw buffer
+// loads (out-of-range offsets read as zero, never fault), MFMA wrappers and
+// fp16/bf16 packing. CDNA4 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kargs.h"
+
+namespace mtk {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+enum { DT_F16 = 0, DT_BF16 = 1 };
+
+// A byte offset that is past every buffer range this library creates (ranges are
+// capped at 2^31 - 256 bytes on the host), so a load from it returns zeros.
+constexpr uint32_t kOOB = 0x7fffff00u;
+
+// Word 3 of a gfx9-family buffer descriptor: raw (untyped) 32-bit data format.
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ u32x2 buf_load8(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load4(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load2(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
+// 32x32x16 MFMA, fp32 accumulate. The operands carry 8 packed 16-bit values per lane.
+template <int DT>
+__device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (DT == DT_F16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (DT == DT_F16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+}
+
+// fp32 -> 16-bit storage, round to nearest even (hardware conversions).
+template <int DT>
+__device__ __forceinline__ uint16_t to_bits(float x) {
+  if constexpr (DT == DT_F16) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  } else {
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float from_bits(uint32_t h) {
+  if constexpr (DT == DT_F16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  } else {
+    return __builtin_bit_cast(float, h << 16);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)to_bits<DT>(lo) | ((uint32_t)to_bits<DT>(hi) << 16);
+}
+
+// v_perm_b32 byte selectors: low 16 bits of x, y -> (x.lo | y.lo << 16); high halves likewise.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x05040100u); }
+__device__ __forceinline__ uint32_t pack_hi(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
+
+// Workgroup id remap so that consecutive logical ids share an XCD: hardware hands
+// workgroup b to XCD (b % 8); XCD x receives its ids in order, so logical id =
+// (ids owned by XCDs before x) + (b / 8). A bijection on [0, n).
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+  const int q = n >> 3, r = n & 7, x = b & 7;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + (b >> 3);
+}
+
+}  // namespace mtk

@@ -1,0 +1,79 @@
+/*
+ * Kernel argument blocks, shared verbatim by the host runtime (runtime.cpp)
+ * and the device code objects (*.hip). Each kernel takes exactly one of these
+ * structs by value; the host passes it through hipModuleLaunchKernel.
+ * Plain C: fixed-width integers and raw device pointers only.
+ */
+#ifndef MTK_KARGS_H
+#define MTK_KARGS_H
+
+#include <stdint.h>
+
+#define MTK_KARGS_VERSION 1
+
+/* Tile-GEMM kernels: plain GEMM (A [M][K] . B, B either [N][K] or [K][N]) and
+ * implicit-GEMM convolution (A = im2col of an NDHWC activation, B = DHWIO
+ * weights viewed as [K][O]), one template. */
+typedef struct {
+  const void *A;    /* GEMM: [M][lda] ; conv: activation NDHWC */
+  const void *B;    /* [N][ldb] (NK) or [K][ldb] (KN) */
+  const void *bias; /* [N] or NULL */
+  void *C;          /* [M][ldc] output (f16/bf16), or NULL when writing partials */
+  float *partial;   /* [split_k][M][N] fp32 partials, or NULL for the direct epilogue */
+  int32_t M, N, K;
+  int32_t lda, ldb, ldc;
+  uint32_t a_bytes, b_bytes; /* buffer-resource ranges: loads at or past these byte offsets return 0 */
+  int32_t tiles_m, tiles_n;
+  int32_t k_tiles;          /* ceil(K / 64) */
+  int32_t k_tiles_per_split;
+  int32_t split_k;
+  int32_t has_bias;
+  /* implicit-GEMM convolution geometry (unused by plain GEMM) */
+  int32_t cN, cD, cH, cW, cC;
+  int32_t cKD, cKH, cKW;
+  int32_t cSZ, cSY, cSX;
+  int32_t cDZ, cDY, cDX;
+  int32_t cPF, cPT, cPL;
+  int32_t cOD, cOH, cOW;
+} mtk_tile_args;
+
+/* Second pass of split-K: out[m][n] = sum_s partial[s][m][n] + bias[n]. */
+typedef struct {
+  const float *partial;
+  const void *bias;
+  void *C;
+  int32_t M, N, ldc;
+  int32_t split_k;
+  int32_t has_bias;
+  int32_t vec8; /* 1: N, ldc multiple of 8 and C, bias 16-byte aligned -> 8-wide path */
+} mtk_reduce_args;
+
+/* Skinny (decode-shaped) GEMM: A [M <= 16][lda], B [N][ldb] (NK), fp32 partials per K split. */
+typedef struct {
+  const void *A;
+  const void *B;
+  const void *bias;
+  void *C;
+  float *partial;
+  int32_t M, N, K;
+  int32_t lda, ldb, ldc;
+  uint32_t a_bytes, b_bytes;
+  int32_t split_k;
+  int32_t k_per_split; /* multiple of the kernel's K step */
+  int32_t has_bias;
+} mtk_skinny_args;
+
+/* Flash-attention forward, Q/K/V/O laid out [B][S][H][D] with D = 128. */
+typedef struct {
+  const void *Q;
+  const void *K;
+  const void *V;
+  void *O;
+  int32_t B, H, S_q, S_kv;
+  int32_t q_blocks;  /* ceil(S_q / query rows per workgroup) */
+  int32_t causal;
+  float scale_log2; /* log2(e) / sqrt(D) */
+  uint32_t q_bytes, kv_bytes;
+} mtk_attn_kargs;
+
+#endif

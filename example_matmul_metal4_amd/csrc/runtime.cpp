@@ -1,0 +1,855 @@
+// Host runtime behind include/mtk.h: device/context, code-object modules, kernel-select
+// (plans), launches through hipModuleLaunchKernel, event timing and error reporting.
+//
+// The reference builds a Metal pipeline per shape by generating MSL source and JIT compiling it
+// (Sources/matmul/matmul.swift:364-390). Here every kernel is compiled ahead of time by
+// `hipcc --genco --offload-arch=gfx950` into mtk_*.hsaco code objects; a plan picks one of the
+// template instantiations by name and fixes its grid and argument block.
+//
+// Plans may be created with ctx == NULL ("dry" plans): the descriptor is validated and the
+// kernel-select is made, but nothing is resolved on a device. That keeps the selection logic
+// testable on machines without a GPU; running a dry plan is an error.
+#include <dirent.h>
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/mtk.h"
+#include "kargs.h"
+
+namespace {
+
+thread_local std::string g_last_error = "no error";
+
+int fail(int status, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+#define HIP_TRY(expr)                                                                       \
+  do {                                                                                      \
+    hipError_t e_ = (expr);                                                                 \
+    if (e_ != hipSuccess) return fail(MTK_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+constexpr uint64_t kMaxOperandBytes = (1ull << 31) - 256;  // buffer-resource ranges (see device.hpp)
+
+}  // namespace
+
+struct mtk_ctx {
+  int device = 0;
+  hipDeviceProp_t prop{};
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  std::vector<hipModule_t> modules;
+  std::map<std::string, hipFunction_t> functions;
+
+  int function(const std::string &name, hipFunction_t *f) {
+    auto it = functions.find(name);
+    if (it != functions.end()) {
+      *f = it->second;
+      return MTK_OK;
+    }
+    for (hipModule_t m : modules) {
+      hipFunction_t fn = nullptr;
+      if (hipModuleGetFunction(&fn, m, name.c_str()) == hipSuccess && fn) {
+        functions[name] = fn;
+        *f = fn;
+        return MTK_OK;
+      }
+    }
+    (void)hipGetLastError();
+    return fail(MTK_ERR_MODULE, "kernel %s not found in the loaded code objects", name.c_str());
+  }
+};
+
+namespace {
+
+enum PlanKind { PLAN_GEMM = 1, PLAN_ATTN = 2, PLAN_CONV = 3 };
+
+struct Launch {
+  std::string name;
+  hipFunction_t fn = nullptr;
+  unsigned grid = 1, block = 256;
+  std::vector<char> args;  // kernel argument block (one struct, by value)
+};
+
+}  // namespace
+
+struct mtk_plan {
+  mtk_ctx *ctx = nullptr;
+  PlanKind kind = PLAN_GEMM;
+  mtk_gemm_desc gemm{};
+  mtk_attn_desc attn{};
+  mtk_conv_desc conv{};
+  std::vector<Launch> launches;
+  size_t workspace = 0;
+  unsigned align_a = 2, align_b = 2;  // required operand alignments (bytes)
+  double flops = 0, bytes = 0;
+  std::string description;
+};
+
+namespace {
+
+int resolve(mtk_plan *p) {
+  if (!p->ctx) return MTK_OK;
+  for (auto &l : p->launches) {
+    int s = p->ctx->function(l.name, &l.fn);
+    if (s != MTK_OK) return s;
+  }
+  return MTK_OK;
+}
+
+template <typename T>
+void set_args(Launch &l, const T &a) {
+  l.args.resize(sizeof(T));
+  memcpy(l.args.data(), &a, sizeof(T));
+}
+
+template <typename T>
+T &args_of(Launch &l) {
+  return *reinterpret_cast<T *>(l.args.data());
+}
+
+int launch_all(const mtk_plan *p, std::vector<Launch> &ls, hipEvent_t *evs) {
+  hipStream_t s = p->ctx->stream;
+  if (evs) HIP_TRY(hipEventRecord(evs[0], s));
+  for (size_t i = 0; i < ls.size(); ++i) {
+    Launch &l = ls[i];
+    void *params[] = {l.args.data()};
+    hipError_t e = hipModuleLaunchKernel(l.fn, l.grid, 1, 1, l.block, 1, 1, 0, s, params, nullptr);
+    if (e != hipSuccess) return fail(MTK_ERR_LAUNCH, "launch of %s failed: %s", l.name.c_str(), hipGetErrorString(e));
+    if (evs) HIP_TRY(hipEventRecord(evs[i + 1], s));
+  }
+  return MTK_OK;
+}
+
+int pow2_vec(std::initializer_list<long long> values) {
+  for (int v : {8, 4, 2}) {
+    bool ok = true;
+    for (long long x : values) ok = ok && (x % v == 0);
+    if (ok) return v == 2 ? 1 : v;  // 2-wide loads are served by the scalar path
+  }
+  return 1;
+}
+
+bool aligned(const void *p, unsigned a) { return ((uintptr_t)p % a) == 0; }
+
+float f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu;
+  if (exp == 0) return (sign ? -1.0f : 1.0f) * std::ldexp((float)mant, -24);
+  const uint32_t u = exp == 31 ? (sign | 0x7f800000u | (mant << 13)) : (sign | ((exp + 112u) << 23) | (mant << 13));
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+float bf16_to_f32(uint16_t h) {
+  const uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// ------------------------------------------------------------------ GEMM planning
+
+int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
+  if (!d_in || !out) return fail(MTK_ERR_INVALID, "null descriptor or output");
+  mtk_gemm_desc d = *d_in;
+  if (d.M <= 0 || d.N <= 0 || d.K <= 0) return fail(MTK_ERR_INVALID, "M, N, K must be positive (got %d, %d, %d)", d.M, d.N, d.K);
+  if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "GEMM dtype must be MTK_F16 or MTK_BF16");
+  if (d.lda == 0) d.lda = d.K;
+  if (d.ldb == 0) d.ldb = d.trans_b ? d.K : d.N;
+  if (d.ldc == 0) d.ldc = d.N;
+  if (d.lda < d.K) return fail(MTK_ERR_INVALID, "lda (%d) < K (%d)", d.lda, d.K);
+  if (d.ldb < (d.trans_b ? d.K : d.N)) return fail(MTK_ERR_INVALID, "ldb (%d) too small", d.ldb);
+  if (d.ldc < d.N) return fail(MTK_ERR_INVALID, "ldc (%d) < N (%d)", d.ldc, d.N);
+  if (d.split_k < 0) return fail(MTK_ERR_INVALID, "split_k must be >= 0");
+  if (d.tile != 0 && d.tile != 128 && d.tile != 256) return fail(MTK_ERR_INVALID, "tile must be 0, 128 or 256");
+  const uint64_t a_bytes = ((uint64_t)(d.M - 1) * d.lda + d.K) * 2;
+  const uint64_t b_rows = d.trans_b ? d.N : d.K, b_cols = d.trans_b ? d.K : d.N;
+  const uint64_t b_bytes = ((b_rows - 1) * (uint64_t)d.ldb + b_cols) * 2;
+  if (a_bytes > kMaxOperandBytes || b_bytes > kMaxOperandBytes)
+    return fail(MTK_ERR_UNSUPPORTED, "operands above 2 GiB are not supported by this build");
+
+  mtk_plan *p = new mtk_plan();
+  p->ctx = ctx;
+  p->kind = PLAN_GEMM;
+  p->gemm = d;
+  const char *dt = d.dtype == MTK_F16 ? "f16" : "bf16";
+  const int k_tiles = (d.K + 63) / 64;
+
+  int tile = d.tile;
+  int split = d.split_k;
+  if (tile == 0) {
+    const long long t256 = (long long)((d.M + 255) / 256) * ((d.N + 255) / 256);
+    tile = (t256 * std::max(split, 1) >= 128) ? 256 : 128;
+  }
+  const int tiles_m = (d.M + tile - 1) / tile, tiles_n = (d.N + tile - 1) / tile;
+  const long long tiles = (long long)tiles_m * tiles_n;
+  if (split == 0) {  // fill about one wave of 256 CUs with split-K when the tile grid is small
+    split = 1;
+    if (tiles < 192) split = (int)std::min<long long>(std::max<long long>(1, 256 / tiles), std::max(1, k_tiles / 4));
+    split = std::min(split, 16);
+  }
+  split = std::min(split, k_tiles);
+  const int kps = (k_tiles + split - 1) / split;
+  split = (k_tiles + kps - 1) / kps;  // no empty splits
+
+  const int v = d.trans_b ? pow2_vec({d.lda, d.ldb, d.K}) : pow2_vec({d.lda, d.K, d.ldb, d.N});
+  p->align_a = p->align_b = 2 * v;
+
+  Launch g;
+  char name[96];
+  snprintf(name, sizeof name, "mtk_gemm_%s_%s_%dx%d_v%d", dt, d.trans_b ? "nt" : "nn", tile, tile, v);
+  g.name = name;
+  g.grid = (unsigned)(tiles * split);
+  mtk_tile_args a{};
+  a.M = d.M;
+  a.N = d.N;
+  a.K = d.K;
+  a.lda = d.lda;
+  a.ldb = d.ldb;
+  a.ldc = d.ldc;
+  a.a_bytes = (uint32_t)a_bytes;
+  a.b_bytes = (uint32_t)b_bytes;
+  a.tiles_m = tiles_m;
+  a.tiles_n = tiles_n;
+  a.k_tiles = k_tiles;
+  a.k_tiles_per_split = kps;
+  a.split_k = split;
+  a.has_bias = d.has_bias ? 1 : 0;
+  set_args(g, a);
+  p->launches.push_back(g);
+  if (split > 1) {
+    p->workspace = (size_t)split * d.M * d.N * sizeof(float);
+    Launch r;
+    r.name = std::string("mtk_splitk_reduce_") + dt;
+    mtk_reduce_args ra{};
+    ra.M = d.M;
+    ra.N = d.N;
+    ra.ldc = d.ldc;
+    ra.split_k = split;
+    ra.has_bias = a.has_bias;
+    ra.vec8 = (d.N % 8 == 0 && d.ldc % 8 == 0) ? 1 : 0;
+    const long long work = ra.vec8 ? (long long)d.M * d.N / 8 : (long long)d.M * d.N;
+    r.grid = (unsigned)std::min<long long>((work + 255) / 256, 2048);
+    set_args(r, ra);
+    p->launches.push_back(r);
+  }
+  p->flops = 2.0 * d.M * d.N * d.K;
+  p->bytes = 2.0 * ((double)d.M * d.K + (double)d.N * d.K + (double)d.M * d.N + (d.has_bias ? d.N : 0));
+  char desc[256];
+  snprintf(desc, sizeof desc, "gemm %s %s M=%d N=%d K=%d tile=%dx%d split_k=%d k_tiles/split=%d vec=%d grid=%u%s",
+           dt, d.trans_b ? "B[N][K]" : "B[K][N]", d.M, d.N, d.K, tile, tile, split, kps, v, g.grid,
+           split > 1 ? " + splitk_reduce" : "");
+  p->description = desc;
+  int s = resolve(p);
+  if (s != MTK_OK) {
+    delete p;
+    return s;
+  }
+  *out = p;
+  return MTK_OK;
+}
+
+// ------------------------------------------------------------------ conv planning
+
+int conv_out(const mtk_conv_desc *d, int *od, int *oh, int *ow) {
+  *od = (d->D + d->pad_front + d->pad_back - ((d->KD - 1) * d->dil_d + 1)) / d->stride_d + 1;
+  *oh = (d->H + d->pad_top + d->pad_bottom - ((d->KH - 1) * d->dil_h + 1)) / d->stride_h + 1;
+  *ow = (d->W + d->pad_left + d->pad_right - ((d->KW - 1) * d->dil_w + 1)) / d->stride_w + 1;
+  return MTK_OK;
+}
+
+int normalise_conv(const mtk_conv_desc *in, mtk_conv_desc *d) {
+  if (!in) return fail(MTK_ERR_INVALID, "null descriptor");
+  *d = *in;
+  if (d->rank == 2) {
+    d->D = 1;
+    d->KD = 1;
+    d->stride_d = d->stride_d > 0 ? d->stride_d : 1;
+    d->dil_d = d->dil_d > 0 ? d->dil_d : 1;
+    if (d->pad_front || d->pad_back) return fail(MTK_ERR_INVALID, "rank-2 convolution has no depth padding");
+  } else if (d->rank != 3) {
+    return fail(MTK_ERR_INVALID, "rank must be 2 or 3 (got %d)", d->rank);
+  }
+  if (d->N <= 0 || d->D <= 0 || d->H <= 0 || d->W <= 0 || d->C <= 0 || d->O <= 0)
+    return fail(MTK_ERR_INVALID, "N, D, H, W, C, O must be positive");
+  if (d->KD <= 0 || d->KH <= 0 || d->KW <= 0) return fail(MTK_ERR_INVALID, "kernel extents must be positive");
+  if (d->KD > 32 || d->KH > 32 || d->KW > 32) return fail(MTK_ERR_UNSUPPORTED, "kernel extents above 32 are not supported");
+  if (d->stride_d <= 0 || d->stride_h <= 0 || d->stride_w <= 0) return fail(MTK_ERR_INVALID, "strides must be positive");
+  if (d->dil_d <= 0 || d->dil_h <= 0 || d->dil_w <= 0) return fail(MTK_ERR_INVALID, "dilations must be positive");
+  if (d->pad_front < 0 || d->pad_back < 0 || d->pad_top < 0 || d->pad_bottom < 0 || d->pad_left < 0 || d->pad_right < 0)
+    return fail(MTK_ERR_INVALID, "padding must be non-negative");
+  if (d->dtype != MTK_F16) return fail(MTK_ERR_INVALID, "convolution dtype must be MTK_F16");
+  int od, oh, ow;
+  conv_out(d, &od, &oh, &ow);
+  if (d->D + d->pad_front + d->pad_back < (d->KD - 1) * d->dil_d + 1 || d->H + d->pad_top + d->pad_bottom < (d->KH - 1) * d->dil_h + 1 ||
+      d->W + d->pad_left + d->pad_right < (d->KW - 1) * d->dil_w + 1 || od <= 0 || oh <= 0 || ow <= 0)
+    return fail(MTK_ERR_INVALID, "kernel larger than the padded input");
+  return MTK_OK;
+}
+
+int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
+  if (!out) return fail(MTK_ERR_INVALID, "null output");
+  mtk_conv_desc d;
+  int s = normalise_conv(d_in, &d);
+  if (s != MTK_OK) return s;
+  int od, oh, ow;
+  conv_out(&d, &od, &oh, &ow);
+  const long long M = (long long)d.N * od * oh * ow;
+  const long long K = (long long)d.KD * d.KH * d.KW * d.C;
+  const uint64_t x_bytes = (uint64_t)d.N * d.D * d.H * d.W * d.C * 2;
+  const uint64_t w_bytes = (uint64_t)K * d.O * 2;
+  const uint64_t y_elems = (uint64_t)M * d.O;
+  if (x_bytes > kMaxOperandBytes || w_bytes > kMaxOperandBytes || M >= (1ll << 31) || y_elems >= (1ull << 40))
+    return fail(MTK_ERR_UNSUPPORTED, "operands above 2 GiB are not supported by this build");
+
+  mtk_plan *p = new mtk_plan();
+  p->ctx = ctx;
+  p->kind = PLAN_CONV;
+  p->conv = d;
+  const bool fast = (d.C % 64) == 0;
+  int va, vb, bm, bn;
+  const char *kind;
+  if (fast) {
+    kind = "fast";
+    va = 8;
+    vb = pow2_vec({d.O});
+    if (d.O >= 256 || d.O % 256 == 0) {
+      bm = 256;
+      bn = 256;
+    } else if (d.O > 64) {
+      bm = 256;
+      bn = 128;
+    } else {
+      bm = 128;
+      bn = 128;
+    }
+    if ((M + bm - 1) / bm * ((d.O + bn - 1) / bn) < 128) bm = bn = 128;
+  } else {
+    kind = "gen";
+    va = vb = pow2_vec({d.C, d.O});
+    bm = bn = 128;
+  }
+  p->align_a = 2 * va;
+  p->align_b = 2 * vb;
+  Launch g;
+  char name[96];
+  if (fast)
+    snprintf(name, sizeof name, "mtk_conv_f16_%s_%dx%d_v%d", kind, bm, bn, vb);
+  else
+    snprintf(name, sizeof name, "mtk_conv_f16_%s_%dx%d_v%d", kind, bm, bn, va);
+  g.name = name;
+  mtk_tile_args a{};
+  a.M = (int)M;
+  a.N = d.O;
+  a.K = (int)K;
+  a.lda = 0;
+  a.ldb = d.O;
+  a.ldc = d.O;
+  a.a_bytes = (uint32_t)x_bytes;
+  a.b_bytes = (uint32_t)w_bytes;
+  a.tiles_m = (int)((M + bm - 1) / bm);
+  a.tiles_n = (d.O + bn - 1) / bn;
+  a.k_tiles = (int)((K + 63) / 64);
+  a.k_tiles_per_split = a.k_tiles;
+  a.split_k = 1;
+  a.has_bias = d.has_bias ? 1 : 0;
+  a.cN = d.N;
+  a.cD = d.D;
+  a.cH = d.H;
+  a.cW = d.W;
+  a.cC = d.C;
+  a.cKD = d.KD;
+  a.cKH = d.KH;
+  a.cKW = d.KW;
+  a.cSZ = d.stride_d;
+  a.cSY = d.stride_h;
+  a.cSX = d.stride_w;
+  a.cDZ = d.dil_d;
+  a.cDY = d.dil_h;
+  a.cDX = d.dil_w;
+  a.cPF = d.pad_front;
+  a.cPT = d.pad_top;
+  a.cPL = d.pad_left;
+  a.cOD = od;
+  a.cOH = oh;
+  a.cOW = ow;
+  g.grid = (unsigned)((long long)a.tiles_m * a.tiles_n);
+  set_args(g, a);
+  p->launches.push_back(g);
+  p->flops = 2.0 * (double)M * d.O * (double)K;
+  p->bytes = (double)x_bytes + (double)w_bytes + 2.0 * (double)y_elems + (d.has_bias ? 2.0 * d.O : 0);
+  char desc[256];
+  snprintf(desc, sizeof desc, "conv%dd f16 implicit-GEMM M=%lld N=%d K=%lld out=%dx%dx%d tile=%dx%d gather=%s grid=%u",
+           d.rank, M, d.O, K, od, oh, ow, bm, bn, kind, g.grid);
+  p->description = desc;
+  s = resolve(p);
+  if (s != MTK_OK) {
+    delete p;
+    return s;
+  }
+  *out = p;
+  return MTK_OK;
+}
+
+// ------------------------------------------------------------------ attention planning
+
+constexpr int kAttnRowsPerWG = 128;  // query rows per workgroup (4 waves x 32)
+
+int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
+  if (!d_in || !out) return fail(MTK_ERR_INVALID, "null descriptor or output");
+  mtk_attn_desc d = *d_in;
+  if (d.B <= 0 || d.H <= 0 || d.S_q <= 0 || d.S_kv <= 0) return fail(MTK_ERR_INVALID, "B, H, S_q, S_kv must be positive");
+  if (d.D != 128) return fail(MTK_ERR_UNSUPPORTED, "head dimension must be 128 (got %d)", d.D);
+  if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "attention dtype must be MTK_F16 or MTK_BF16");
+  const uint64_t q_bytes = (uint64_t)d.B * d.S_q * d.H * d.D * 2;
+  const uint64_t kv_bytes = (uint64_t)d.B * d.S_kv * d.H * d.D * 2;
+  if (q_bytes > kMaxOperandBytes || kv_bytes > kMaxOperandBytes)
+    return fail(MTK_ERR_UNSUPPORTED, "operands above 2 GiB are not supported by this build");
+  mtk_plan *p = new mtk_plan();
+  p->ctx = ctx;
+  p->kind = PLAN_ATTN;
+  p->attn = d;
+  p->align_a = p->align_b = 16;
+  Launch g;
+  g.name = std::string("mtk_attn_fwd_") + (d.dtype == MTK_F16 ? "f16" : "bf16") + (d.causal ? "_causal" : "");
+  mtk_attn_kargs a{};
+  a.B = d.B;
+  a.H = d.H;
+  a.S_q = d.S_q;
+  a.S_kv = d.S_kv;
+  a.q_blocks = (d.S_q + kAttnRowsPerWG - 1) / kAttnRowsPerWG;
+  a.causal = d.causal ? 1 : 0;
+  a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)d.D));
+  a.q_bytes = (uint32_t)q_bytes;
+  a.kv_bytes = (uint32_t)kv_bytes;
+  g.grid = (unsigned)((long long)a.q_blocks * d.B * d.H);
+  set_args(g, a);
+  p->launches.push_back(g);
+  double pairs = (double)d.S_q * d.S_kv;
+  if (d.causal) {  // exact count of unmasked (i, j): j <= i + (S_kv - S_q)
+    pairs = 0;
+    for (long long i = 0; i < d.S_q; ++i) {
+      long long lim = i + (d.S_kv - d.S_q) + 1;
+      pairs += (double)std::max(0ll, std::min<long long>(lim, d.S_kv));
+    }
+  }
+  p->flops = 4.0 * d.B * d.H * d.D * pairs;
+  p->bytes = 2.0 * (double)q_bytes + 2.0 * (double)kv_bytes;
+  char desc[256];
+  snprintf(desc, sizeof desc, "attention fwd %s B=%d H=%d S_q=%d S_kv=%d D=%d causal=%d rows/wg=%d grid=%u",
+           d.dtype == MTK_F16 ? "f16" : "bf16", d.B, d.H, d.S_q, d.S_kv, d.D, d.causal, kAttnRowsPerWG, g.grid);
+  p->description = desc;
+  int s = resolve(p);
+  if (s != MTK_OK) {
+    delete p;
+    return s;
+  }
+  *out = p;
+  return MTK_OK;
+}
+
+// ------------------------------------------------------------------ binding run-time pointers
+
+int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
+  ls = p->launches;
+  if (p->kind == PLAN_GEMM) {
+    const mtk_gemm_args *g = (const mtk_gemm_args *)argset;
+    if (!g || !g->A || !g->B || !g->C) return fail(MTK_ERR_INVALID, "A, B and C must be non-null");
+    if (p->gemm.has_bias && !g->bias) return fail(MTK_ERR_INVALID, "plan has a bias but bias is null");
+    if (!aligned(g->A, p->align_a) || !aligned(g->B, p->align_b))
+      return fail(MTK_ERR_INVALID, "A/B must be %u-byte aligned for this plan", p->align_a);
+    if (p->workspace && (!g->workspace || !aligned(g->workspace, 16)))
+      return fail(MTK_ERR_INVALID, "this plan needs a 16-byte aligned workspace of %zu bytes", p->workspace);
+    mtk_tile_args &a = args_of<mtk_tile_args>(ls[0]);
+    a.A = g->A;
+    a.B = g->B;
+    a.bias = g->bias;
+    if (ls.size() > 1) {
+      a.C = nullptr;
+      a.partial = (float *)g->workspace;
+      mtk_reduce_args &r = args_of<mtk_reduce_args>(ls[1]);
+      r.partial = (const float *)g->workspace;
+      r.bias = g->bias;
+      r.C = g->C;
+      r.vec8 = r.vec8 && aligned(g->C, 16) && (!g->bias || aligned(g->bias, 16));
+    } else {
+      a.C = g->C;
+      a.partial = nullptr;
+    }
+  } else if (p->kind == PLAN_CONV) {
+    const mtk_conv_args *c = (const mtk_conv_args *)argset;
+    if (!c || !c->x || !c->w || !c->y) return fail(MTK_ERR_INVALID, "x, w and y must be non-null");
+    if (p->conv.has_bias && !c->bias) return fail(MTK_ERR_INVALID, "plan has a bias but bias is null");
+    if (!aligned(c->x, p->align_a) || !aligned(c->w, p->align_b))
+      return fail(MTK_ERR_INVALID, "x must be %u-byte and w %u-byte aligned for this plan", p->align_a, p->align_b);
+    mtk_tile_args &a = args_of<mtk_tile_args>(ls[0]);
+    a.A = c->x;
+    a.B = c->w;
+    a.bias = c->bias;
+    a.C = c->y;
+    a.partial = nullptr;
+  } else {
+    const mtk_attn_args *t = (const mtk_attn_args *)argset;
+    if (!t || !t->Q || !t->K || !t->V || !t->O) return fail(MTK_ERR_INVALID, "Q, K, V and O must be non-null");
+    if (!aligned(t->Q, 16) || !aligned(t->K, 16) || !aligned(t->V, 16) || !aligned(t->O, 16))
+      return fail(MTK_ERR_INVALID, "Q, K, V, O must be 16-byte aligned");
+    mtk_attn_kargs &a = args_of<mtk_attn_kargs>(ls[0]);
+    a.Q = t->Q;
+    a.K = t->K;
+    a.V = t->V;
+    a.O = t->O;
+  }
+  return MTK_OK;
+}
+
+size_t argset_size(const mtk_plan *p) {
+  switch (p->kind) {
+    case PLAN_GEMM:
+      return sizeof(mtk_gemm_args);
+    case PLAN_CONV:
+      return sizeof(mtk_conv_args);
+    default:
+      return sizeof(mtk_attn_args);
+  }
+}
+
+int run_plan(const mtk_plan *p, const void *argset) {
+  if (!p) return fail(MTK_ERR_INVALID, "null plan");
+  if (!p->ctx) return fail(MTK_ERR_INVALID, "plan was created without a context (dry plan)");
+  std::vector<Launch> ls;
+  int s = bind_args(p, argset, ls);
+  if (s != MTK_OK) return s;
+  HIP_TRY(hipSetDevice(p->ctx->device));
+  return launch_all(p, ls, nullptr);
+}
+
+std::string self_dir() {
+  Dl_info info;
+  if (dladdr((void *)&mtk_init, &info) && info.dli_fname) {
+    std::string f = info.dli_fname;
+    size_t k = f.rfind('/');
+    if (k != std::string::npos) return f.substr(0, k);
+  }
+  return ".";
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+extern "C" {
+
+const char *mtk_last_error(void) { return g_last_error.c_str(); }
+
+const char *mtk_status_string(int s) {
+  switch (s) {
+    case MTK_OK:
+      return "MTK_OK";
+    case MTK_ERR_INVALID:
+      return "MTK_ERR_INVALID";
+    case MTK_ERR_NO_DEVICE:
+      return "MTK_ERR_NO_DEVICE";
+    case MTK_ERR_UNSUPPORTED:
+      return "MTK_ERR_UNSUPPORTED";
+    case MTK_ERR_MODULE:
+      return "MTK_ERR_MODULE";
+    case MTK_ERR_OOM:
+      return "MTK_ERR_OOM";
+    case MTK_ERR_LAUNCH:
+      return "MTK_ERR_LAUNCH";
+    case MTK_ERR_HIP:
+      return "MTK_ERR_HIP";
+    default:
+      return "unknown status";
+  }
+}
+
+int mtk_device_count(int *count) {
+  if (!count) return fail(MTK_ERR_INVALID, "null count");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    *count = 0;
+    return fail(MTK_ERR_NO_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+  }
+  *count = n;
+  return MTK_OK;
+}
+
+int mtk_init(int device, const char *code_object_dir, mtk_ctx **out) {
+  if (!out) return fail(MTK_ERR_INVALID, "null output");
+  *out = nullptr;
+  int n = 0;
+  int s = mtk_device_count(&n);
+  if (s != MTK_OK) return s;
+  if (n <= 0) return fail(MTK_ERR_NO_DEVICE, "no HIP device");
+  if (device < 0 || device >= n) return fail(MTK_ERR_INVALID, "device %d out of range (%d devices)", device, n);
+  mtk_ctx *ctx = new mtk_ctx();
+  ctx->device = device;
+  auto bail = [&](int status) {
+    mtk_destroy(ctx);
+    return status;
+  };
+  if (hipSetDevice(device) != hipSuccess) return bail(fail(MTK_ERR_HIP, "hipSetDevice(%d) failed", device));
+  if (hipGetDeviceProperties(&ctx->prop, device) != hipSuccess) return bail(fail(MTK_ERR_HIP, "hipGetDeviceProperties failed"));
+  if (strncmp(ctx->prop.gcnArchName, "gfx950", 6) != 0)
+    return bail(fail(MTK_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950 (MI355X)", device, ctx->prop.gcnArchName));
+  if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess)
+    return bail(fail(MTK_ERR_HIP, "hipStreamCreate failed"));
+  ctx->stream = ctx->own_stream;
+  std::string dir;
+  if (code_object_dir && *code_object_dir)
+    dir = code_object_dir;
+  else if (const char *env = getenv("MTK_CODE_OBJECT_DIR"))
+    dir = env;
+  else
+    dir = self_dir();
+  DIR *dp = opendir(dir.c_str());
+  if (!dp) return bail(fail(MTK_ERR_MODULE, "code object directory %s not readable", dir.c_str()));
+  std::vector<std::string> files;
+  while (dirent *e = readdir(dp)) {
+    std::string f = e->d_name;
+    if (f.size() > 10 && f.rfind("mtk_", 0) == 0 && f.substr(f.size() - 6) == ".hsaco") files.push_back(f);
+  }
+  closedir(dp);
+  std::sort(files.begin(), files.end());
+  if (files.empty()) return bail(fail(MTK_ERR_MODULE, "no mtk_*.hsaco code objects in %s", dir.c_str()));
+  for (const std::string &f : files) {
+    hipModule_t m = nullptr;
+    std::string path = dir + "/" + f;
+    hipError_t e = hipModuleLoad(&m, path.c_str());
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return bail(fail(MTK_ERR_MODULE, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e)));
+    }
+    ctx->modules.push_back(m);
+  }
+  *out = ctx;
+  return MTK_OK;
+}
+
+int mtk_destroy(mtk_ctx *ctx) {
+  if (!ctx) return MTK_OK;
+  if (ctx->own_stream) {
+    (void)hipStreamSynchronize(ctx->own_stream);
+    (void)hipStreamDestroy(ctx->own_stream);
+  }
+  for (hipModule_t m : ctx->modules) (void)hipModuleUnload(m);
+  delete ctx;
+  return MTK_OK;
+}
+
+int mtk_get_device_info(const mtk_ctx *ctx, mtk_device_info *info) {
+  if (!ctx || !info) return fail(MTK_ERR_INVALID, "null argument");
+  memset(info, 0, sizeof *info);
+  snprintf(info->name, sizeof info->name, "%s", ctx->prop.name);
+  snprintf(info->arch, sizeof info->arch, "%s", ctx->prop.gcnArchName);
+  info->compute_units = ctx->prop.multiProcessorCount;
+  info->clock_khz = ctx->prop.clockRate;
+  info->lds_bytes_per_cu = (int)ctx->prop.maxSharedMemoryPerMultiProcessor;
+  info->wavefront_size = ctx->prop.warpSize;
+  info->global_mem_bytes = ctx->prop.totalGlobalMem;
+  info->peak_f16_tflops = (double)info->compute_units * (info->clock_khz * 1e3) * 4096.0 / 1e12;
+  return MTK_OK;
+}
+
+int mtk_alloc(mtk_ctx *ctx, size_t bytes, void **dptr) {
+  if (!ctx || !dptr) return fail(MTK_ERR_INVALID, "null argument");
+  *dptr = nullptr;
+  HIP_TRY(hipSetDevice(ctx->device));
+  hipError_t e = hipMalloc(dptr, bytes ? bytes : 1);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MTK_ERR_OOM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+  }
+  return MTK_OK;
+}
+
+int mtk_free(mtk_ctx *ctx, void *dptr) {
+  if (!ctx) return fail(MTK_ERR_INVALID, "null context");
+  if (!dptr) return MTK_OK;
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipFree(dptr));
+  return MTK_OK;
+}
+
+int mtk_upload(mtk_ctx *ctx, void *dst, const void *src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(MTK_ERR_INVALID, "null argument");
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return MTK_OK;
+}
+
+int mtk_download(mtk_ctx *ctx, void *dst, const void *src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(MTK_ERR_INVALID, "null argument");
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return MTK_OK;
+}
+
+int mtk_fill_u16(mtk_ctx *ctx, void *dst, uint16_t value, size_t count) {
+  if (!ctx || (!dst && count)) return fail(MTK_ERR_INVALID, "null argument");
+  if (!count) return MTK_OK;
+  hipFunction_t f;
+  int s = ctx->function("mtk_fill_u16", &f);
+  if (s != MTK_OK) return s;
+  struct {
+    void *p;
+    uint64_t n;
+    uint32_t v;
+  } a{dst, count, value};
+  void *params[] = {&a};
+  unsigned grid = (unsigned)std::min<size_t>((count + 255) / 256, 4096);
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipModuleLaunchKernel(f, grid, 1, 1, 256, 1, 1, 0, ctx->stream, params, nullptr));
+  return MTK_OK;
+}
+
+int mtk_sync(mtk_ctx *ctx) {
+  if (!ctx) return fail(MTK_ERR_INVALID, "null context");
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return MTK_OK;
+}
+
+int mtk_set_stream(mtk_ctx *ctx, void *hip_stream) {
+  if (!ctx) return fail(MTK_ERR_INVALID, "null context");
+  ctx->stream = hip_stream ? (hipStream_t)hip_stream : ctx->own_stream;
+  return MTK_OK;
+}
+
+int mtk_gemm_plan(mtk_ctx *ctx, const mtk_gemm_desc *desc, mtk_plan **out) { return plan_gemm(ctx, desc, out); }
+int mtk_gemm_run(const mtk_plan *plan, const mtk_gemm_args *args) {
+  if (plan && plan->kind != PLAN_GEMM) return fail(MTK_ERR_INVALID, "not a GEMM plan");
+  return run_plan(plan, args);
+}
+
+int mtk_attn_plan(mtk_ctx *ctx, const mtk_attn_desc *desc, mtk_plan **out) { return plan_attn(ctx, desc, out); }
+int mtk_attn_run(const mtk_plan *plan, const mtk_attn_args *args) {
+  if (plan && plan->kind != PLAN_ATTN) return fail(MTK_ERR_INVALID, "not an attention plan");
+  return run_plan(plan, args);
+}
+
+int mtk_conv_plan(mtk_ctx *ctx, const mtk_conv_desc *desc, mtk_plan **out) { return plan_conv(ctx, desc, out); }
+int mtk_conv_out_shape(const mtk_conv_desc *desc, int *OD, int *OH, int *OW) {
+  if (!desc || !OD || !OH || !OW) return fail(MTK_ERR_INVALID, "null argument");
+  mtk_conv_desc d;
+  int s = normalise_conv(desc, &d);
+  if (s != MTK_OK) return s;
+  return conv_out(&d, OD, OH, OW);
+}
+int mtk_conv_run(const mtk_plan *plan, const mtk_conv_args *args) {
+  if (plan && plan->kind != PLAN_CONV) return fail(MTK_ERR_INVALID, "not a convolution plan");
+  return run_plan(plan, args);
+}
+
+size_t mtk_plan_workspace_bytes(const mtk_plan *plan) { return plan ? plan->workspace : 0; }
+
+int mtk_plan_describe(const mtk_plan *plan, char *buf, size_t len) {
+  if (!plan || !buf || !len) return fail(MTK_ERR_INVALID, "null argument");
+  std::string s = plan->description + " kernels:";
+  for (const auto &l : plan->launches) s += " " + l.name;
+  snprintf(buf, len, "%s", s.c_str());
+  return MTK_OK;
+}
+
+int mtk_plan_work(const mtk_plan *plan, double *flops, double *bytes) {
+  if (!plan) return fail(MTK_ERR_INVALID, "null plan");
+  if (flops) *flops = plan->flops;
+  if (bytes) *bytes = plan->bytes;
+  return MTK_OK;
+}
+
+int mtk_plan_destroy(mtk_plan *plan) {
+  delete plan;
+  return MTK_OK;
+}
+
+int mtk_profile(const mtk_plan *p, const void *arg_sets, int nsets, int warmup, int iters, mtk_timing *out) {
+  if (!p || !arg_sets || nsets <= 0 || warmup < 0 || iters <= 0 || !out)
+    return fail(MTK_ERR_INVALID, "invalid profile arguments");
+  if (!p->ctx) return fail(MTK_ERR_INVALID, "plan was created without a context (dry plan)");
+  if (iters > 100000) return fail(MTK_ERR_INVALID, "iters above 100000");
+  memset(out, 0, sizeof *out);
+  const size_t stride = argset_size(p);
+  std::vector<std::vector<Launch>> bound((size_t)nsets);
+  for (int i = 0; i < nsets; ++i) {
+    int s = bind_args(p, (const char *)arg_sets + stride * i, bound[(size_t)i]);
+    if (s != MTK_OK) return s;
+  }
+  HIP_TRY(hipSetDevice(p->ctx->device));
+  for (int i = 0; i < warmup; ++i) {
+    int s = launch_all(p, bound[(size_t)(i % nsets)], nullptr);
+    if (s != MTK_OK) return s;
+  }
+  const size_t nk = p->launches.size();
+  std::vector<hipEvent_t> evs((size_t)iters * (nk + 1));
+  for (auto &e : evs) HIP_TRY(hipEventCreate(&e));
+  int status = MTK_OK;
+  for (int i = 0; i < iters && status == MTK_OK; ++i)
+    status = launch_all(p, bound[(size_t)(i % nsets)], &evs[(size_t)i * (nk + 1)]);
+  if (status == MTK_OK) {
+    hipError_t e = hipStreamSynchronize(p->ctx->stream);
+    if (e != hipSuccess) status = fail(MTK_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+  }
+  if (status == MTK_OK) {
+    std::vector<double> per(nk, 0.0);
+    for (int i = 0; i < iters; ++i) {
+      for (size_t k = 0; k < nk; ++k) {
+        float ms = 0;
+        (void)hipEventElapsedTime(&ms, evs[(size_t)i * (nk + 1) + k], evs[(size_t)i * (nk + 1) + k + 1]);
+        per[k] += ms;
+      }
+    }
+    float total = 0;
+    (void)hipEventElapsedTime(&total, evs[0], evs[(size_t)(iters - 1) * (nk + 1) + nk]);
+    out->total_ms = total / iters;
+    out->n_kernels = (int)std::min<size_t>(nk, 4);
+    for (size_t k = 0; k < nk && k < 4; ++k) {
+      out->kernel_ms[k] = per[k] / iters;
+      snprintf(out->kernel_names[k], sizeof out->kernel_names[k], "%s", p->launches[k].name.c_str());
+    }
+  }
+  for (auto &e : evs) (void)hipEventDestroy(e);
+  return status;
+}
+
+int mtk_validate_f16(const uint16_t *actual, int dtype, const float *expected, size_t n, double abs_tol, mtk_validation *out) {
+  if ((!actual || !expected) && n) return fail(MTK_ERR_INVALID, "null argument");
+  if (!out || (dtype != MTK_F16 && dtype != MTK_BF16)) return fail(MTK_ERR_INVALID, "invalid argument");
+  double num = 0, den = 0, mx = 0;
+  long long bad = 0;
+  for (size_t i = 0; i < n; ++i) {
+    const float v = dtype == MTK_BF16 ? bf16_to_f32(actual[i]) : f16_to_f32(actual[i]);
+    const double diff = std::fabs((double)v - (double)expected[i]);
+    num += diff * diff;
+    den += (double)expected[i] * expected[i];
+    mx = std::max(mx, diff);
+    if (diff > abs_tol || std::isnan(v)) ++bad;
+  }
+  out->rel_frobenius = den > 0 ? std::sqrt(num / den) : std::sqrt(num);
+  out->max_abs_error = mx;
+  out->mismatches = bad;
+  return MTK_OK;
+}
+
+}  // extern "C"

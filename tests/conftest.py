@@ -24,3 +24,16 @@ def orc():
 @pytest.fixture(scope="session")
 def golden_dir():
     return os.path.join(ROOT, "tests", "golden")
+
+
+@pytest.fixture(scope="session")
+def dev():
+    """The gfx950 device context (GPU tests only). No fallback: fails if the library is missing."""
+    import example_matmul_metal4_amd as mtk
+
+    d = mtk.Device(0)
+    info = d.info
+    print(f"\n[device] {info['name']} {info['arch']} CUs={info['compute_units']} clock={info['clock_khz']} kHz",
+          flush=True)
+    yield d
+    d.close()

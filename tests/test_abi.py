@@ -1,0 +1,178 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point include/mtk.h
+declares, refuses to start without a gfx950 device, and its kernel-select / descriptor
+validation (dry plans, ctx = NULL) behaves as documented."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import example_matmul_metal4_amd as mtk
+import oracle
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mtk.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mtk_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    return mtk.lib()
+
+
+def test_exports_every_declared_symbol(L):
+    syms = declared_symbols()
+    assert len(syms) >= 25
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+    # ...and the Python binding types every one of them
+    assert set(syms) <= set(mtk.SIGNATURES), set(syms) - set(mtk.SIGNATURES)
+
+
+def test_code_objects_hold_every_selectable_kernel():
+    blobs = b"".join(open(os.path.join(mtk.LIB_DIR, f), "rb").read()
+                     for f in os.listdir(mtk.LIB_DIR) if f.endswith(".hsaco"))
+    names = [f"mtk_gemm_{dt}_{lay}_{t}x{t}_v{v}" for dt in ("f16", "bf16") for lay in ("nt", "nn")
+             for t in (128, 256) for v in (8, 4, 1)]
+    names += ["mtk_splitk_reduce_f16", "mtk_splitk_reduce_bf16", "mtk_fill_u16"]
+    names += [f"mtk_conv_f16_fast_{t}_v{v}" for t in ("256x256", "256x128", "128x128") for v in (8, 4, 1)]
+    names += [f"mtk_conv_f16_gen_128x128_v{v}" for v in (8, 4, 1)]
+    missing = [n for n in names if n.encode() not in blobs]
+    assert not missing, missing
+
+
+def test_init_without_gpu_reports_no_device(L):
+    n = ctypes.c_int(-1)
+    st = L.mtk_device_count(ctypes.byref(n))
+    if st == mtk.MTK_OK and n.value > 0:
+        pytest.skip("a GPU is visible")
+    h = ctypes.c_void_p()
+    assert L.mtk_init(0, None, ctypes.byref(h)) == mtk.MTK_ERR_NO_DEVICE
+    assert h.value is None
+    assert L.mtk_last_error()
+    with pytest.raises(mtk.MtkError) as e:
+        mtk.Device()
+    assert e.value.status == mtk.MTK_ERR_NO_DEVICE
+
+
+def test_status_strings(L):
+    for s in range(-7, 1):
+        assert L.mtk_status_string(s).startswith(b"MTK_")
+
+
+def test_gemm_kernel_select_dry():
+    p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4)
+    d = p.describe()
+    assert "mtk_gemm_f16_nt_256x256_v4" in d and "mtk_splitk_reduce_f16" in d and "split_k=4" in d
+    assert p.workspace_bytes == 4 * 4096 * 4096 * 4
+    flops, byts = p.work()
+    assert flops == 2 * 4096 * 4096 * 4100 and byts == 2 * (4096 * 4100 * 2 + 4096 * 4096 + 4096)
+    p = mtk.GemmPlan(None, 256, 256, 256, trans_b=False)
+    assert "mtk_gemm_f16_nn_128x128_v8" in p.describe() and p.workspace_bytes == 0
+    p = mtk.GemmPlan(None, 48, 40, 70, dtype="bf16", trans_b=True)
+    assert "mtk_gemm_bf16_nt_128x128_v1" in p.describe()
+    # the K tail is owned by exactly one split: 65 K-tiles over 4 splits -> 17 per split, 4 splits
+    p = mtk.GemmPlan(None, 512, 512, 4100, split_k=4)
+    assert "split_k=4 k_tiles/split=17" in p.describe()
+    # split-K never produces an empty split
+    p = mtk.GemmPlan(None, 64, 64, 100, split_k=8)
+    assert "split_k=2 k_tiles/split=1" in p.describe()
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(M=0, N=4, K=4), mtk.MTK_ERR_INVALID),
+    (dict(M=4, N=4, K=-1), mtk.MTK_ERR_INVALID),
+    (dict(M=4, N=4, K=8, lda=4), mtk.MTK_ERR_INVALID),
+    (dict(M=4, N=4, K=8, ldc=2), mtk.MTK_ERR_INVALID),
+    (dict(M=4, N=4, K=8, split_k=-2), mtk.MTK_ERR_INVALID),
+    (dict(M=4, N=4, K=8, tile=64), mtk.MTK_ERR_INVALID),
+    (dict(M=70000, N=4, K=20000), mtk.MTK_ERR_UNSUPPORTED),
+])
+def test_gemm_descriptor_validation(kw, status):
+    M, N, K = kw.pop("M"), kw.pop("N"), kw.pop("K")
+    with pytest.raises(mtk.MtkError) as e:
+        mtk.GemmPlan(None, M, N, K, **kw)
+    assert e.value.status == status and e.value.message
+
+
+def test_gemm_bad_dtype(L):
+    d = mtk.GemmDesc(M=4, N=4, K=4, dtype=7)
+    h = ctypes.c_void_p()
+    assert L.mtk_gemm_plan(None, ctypes.byref(d), ctypes.byref(h)) == mtk.MTK_ERR_INVALID
+    assert b"dtype" in L.mtk_last_error()
+
+
+def test_dry_plan_refuses_to_run():
+    p = mtk.GemmPlan(None, 64, 64, 64)
+    with pytest.raises(mtk.MtkError) as e:
+        p.run(0x1000, 0x1000, None, 0x1000)
+    assert e.value.status == mtk.MTK_ERR_INVALID
+
+
+def test_conv_kernel_select_and_shapes():
+    d = oracle.ConvDims.conv2d(N=8, H=128, W=128, C=256, O=256, PT=1, PB=1, PL=1, PR=1)
+    p = mtk.ConvPlan(None, mtk.conv_desc(d, has_bias=True))
+    assert "mtk_conv_f16_fast_256x256_v8" in p.describe()
+    assert p.out_shape() == (8, 128, 128, 256)
+    assert p.work()[0] == d.flops() == 154618822656
+    d3 = oracle.ConvDims.conv3d(N=1, D=16, H=64, W=64, C=128, O=128, PF=1, PBk=1, PT=1, PB=1, PL=1, PR=1)
+    p = mtk.ConvPlan(None, mtk.conv_desc(d3))
+    assert "mtk_conv_f16_fast_256x128_v8" in p.describe() and p.out_shape() == (1, 16, 64, 64, 128)
+    assert p.work()[0] == d3.flops() == 57982058496
+    # the reference's case lists: every output shape agrees with the oracle's formulas
+    import json
+    cases = json.load(open(os.path.join(ROOT, "tests", "golden", "cases.json")))
+    for kind, spec in cases.items():
+        for c in spec["cases"]:
+            dims = oracle.ConvDims.conv2d(**c) if "2d" in kind else oracle.ConvDims.conv3d(**c)
+            p = mtk.ConvPlan(None, mtk.conv_desc(dims))
+            shape = p.out_shape()
+            assert shape[1:-1] == ((dims.OH, dims.OW) if len(shape) == 4 else (dims.OD, dims.OH, dims.OW))
+            assert "gen_128x128" in p.describe()
+
+
+@pytest.mark.parametrize("field,value,status", [
+    ("rank", 4, mtk.MTK_ERR_INVALID), ("C", 0, mtk.MTK_ERR_INVALID), ("stride_h", 0, mtk.MTK_ERR_INVALID),
+    ("pad_left", -1, mtk.MTK_ERR_INVALID), ("KH", 40, mtk.MTK_ERR_UNSUPPORTED), ("H", 1, mtk.MTK_ERR_INVALID),
+    ("dtype", mtk.BF16, mtk.MTK_ERR_INVALID), ("pad_front", 1, mtk.MTK_ERR_INVALID),
+])
+def test_conv_descriptor_validation(field, value, status):
+    desc = mtk.conv_desc(oracle.ConvDims.conv2d(N=1, H=5, W=5, C=4, O=8))
+    setattr(desc, field, value)
+    with pytest.raises(mtk.MtkError) as e:
+        mtk.ConvPlan(None, desc)
+    assert e.value.status == status
+
+
+def test_attention_select_and_validation():
+    p = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128, causal=True)
+    assert "mtk_attn_fwd_f16_causal" in p.describe()
+    flops = p.work()[0]
+    assert flops == 4 * 2 * 32 * 128 * (4096 * 4097 // 2)
+    assert mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128).work()[0] == 549755813888
+    with pytest.raises(mtk.MtkError) as e:
+        mtk.AttentionPlan(None, 1, 1, 16, 16, 64)
+    assert e.value.status == mtk.MTK_ERR_UNSUPPORTED
+    with pytest.raises(mtk.MtkError) as e:
+        mtk.AttentionPlan(None, 0, 1, 16, 16, 128)
+    assert e.value.status == mtk.MTK_ERR_INVALID
+
+
+def test_validate_helper_matches_numpy():
+    rng = np.random.default_rng(0)
+    e = rng.standard_normal(1000).astype(np.float32)
+    a = (e + rng.standard_normal(1000).astype(np.float32) * 1e-3).astype(np.float16)
+    r = mtk.validate(a, e, abs_tol=2e-3)
+    af = a.astype(np.float64)
+    assert abs(r["max_abs_error"] - np.abs(af - e).max()) < 1e-12
+    assert r["mismatches"] == int((np.abs(af - e) > 2e-3).sum())
+    assert abs(r["rel_frobenius"] - oracle.rel_frobenius(af, e)) < 1e-12
+    b = oracle.from_f32(e, "bf16")
+    rb = mtk.validate(b, e, abs_tol=0.0, dtype="bf16")
+    assert abs(rb["max_abs_error"] - np.abs(oracle.to_f32(b, "bf16") - e).max()) < 1e-12

@@ -1,0 +1,173 @@
+"""GEMM parity on the GPU, through the C ABI, against the CPU oracle (matmul.swift:498-510).
+
+Acceptance (written out per test): relative Frobenius error <= 1e-3 and, element-wise,
+|y - yhat| <= ulp_out(|yhat|) + 2 * K * 2^-24 * sum_k |a_k b_k| (oracle.dot_bound).
+For bf16 outputs the Frobenius bar is 1e-3 plus the error of rounding the oracle itself to bf16
+(a bf16 output alone carries ~1.1-1.7e-3 relative RMS rounding error, more than 1e-3)."""
+import numpy as np
+import pytest
+
+import example_matmul_metal4_amd as mtk
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _f32(x, dtype):
+    return oracle.to_f32(x, dtype).astype(np.float64)
+
+
+def check(dev, A, B, bias, *, trans_b=True, dtype="f16", split_k=1, tile=0, rows=None, label=""):
+    print(f"[gemm] {label} A{A.shape} B{B.shape} trans_b={trans_b} {dtype} split_k={split_k} tile={tile}", flush=True)
+    got = mtk.gemm(dev, A, B, bias, trans_b=trans_b, dtype=dtype, split_k=split_k, tile=tile)
+    exp = oracle.gemm(A, B, bias, trans_b=trans_b, dtype=dtype, rows=rows)
+    a, b = _f32(A, dtype), _f32(B, dtype)
+    if rows is not None:
+        sel = slice(*rows)
+        got, exp, a = got[sel], exp[sel], a[sel]
+    absdot = np.abs(a) @ (np.abs(b).T if trans_b else np.abs(b))
+    if bias is not None:
+        absdot = absdot + np.abs(_f32(bias, dtype))
+    rel_tol = 1e-3 + (oracle.rel_frobenius(oracle.to_f32(oracle.from_f32(exp, dtype), dtype), exp)
+                      if dtype == "bf16" else 0.0)
+    res = oracle.compare(_f32(got, dtype), exp, bound=oracle.dot_bound(exp, absdot, A.shape[1], dtype),
+                         rel_tol=rel_tol)
+    ref_tol = mtk.validate(got, exp, abs_tol=5e-3, dtype=dtype)  # the reference's own check, reported
+    print(f"   rel_fro={res['rel_fro']:.3e} max_abs={res['max_abs']:.3e} worst/bound={res.get('worst_ratio', 0):.3f} "
+          f"ref5e-3_mismatches={ref_tol['mismatches']}", flush=True)
+    assert res["ok"], res
+    return got, exp
+
+
+def test_config1_256_cubed_nn_seed0(dev):
+    # fp16 C = A.B, M=N=K=256, row-major, A and B from one U[-1,1) stream, seed 0.
+    AB = oracle.uniform(0, (2, 256, 256), -1.0, 1.0)
+    check(dev, AB[0], AB[1], None, trans_b=False, label="config1")
+
+
+def test_fixtures(dev, golden_dir):
+    fx = np.load(f"{golden_dir}/seeded.npz")
+    got = mtk.gemm(dev, fx["gemm_nn_A"], fx["gemm_nn_B"], None, trans_b=False)
+    assert oracle.compare(got.astype(np.float32), fx["gemm_nn_C"])["ok"]
+    got = mtk.gemm(dev, fx["gemm_nt_A"], fx["gemm_nt_B"], fx["gemm_nt_bias"], trans_b=True)
+    assert oracle.compare(got.astype(np.float32), fx["gemm_nt_C"])["ok"]
+    got = mtk.gemm(dev, fx["gemm_bf16_A"], fx["gemm_bf16_B"], fx["gemm_bf16_bias"], trans_b=True, dtype="bf16")
+    assert oracle.compare(oracle.to_f32(got, "bf16"), fx["gemm_bf16_C"], rel_tol=5e-3)["ok"]
+
+
+@pytest.mark.parametrize("split_k", [1, 4, 5])
+def test_all_ones_k4100_exact(dev, split_k):
+    # fp32 sum = K + bias exactly; the f16 output is its round-to-nearest-even (4100 itself is
+    # representable). The reference's split-K tail bug (matmul.swift:266-277 outside the split
+    # branches) would give 4112 + bias with split-K = 4.
+    M, N, K = 64, 96, 4100
+    A = np.ones((M, K), np.float16)
+    B = np.ones((N, K), np.float16)
+    bias = np.arange(-8, N - 8, dtype=np.float16)
+    got = mtk.gemm(dev, A, B, bias, split_k=split_k)
+    exp = (K + bias.astype(np.float32)).astype(np.float16)
+    assert np.array_equal(got, np.broadcast_to(exp, (M, N)))
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 7, 16, 31, 33, 63, 64, 65, 127, 129, 200, 255, 257, 300])
+@pytest.mark.parametrize("trans_b", [True, False])
+def test_cube_sweep(dev, n, trans_b):
+    # mirrors profileCorrectness (matmul.swift:338-343): M = N = K = i
+    A = oracle.uniform(100 + n, (n, n), -1, 1)
+    B = oracle.uniform(200 + n, (n, n), -1, 1)
+    bias = oracle.uniform(300 + n, (n,), -0.5, 0.5)
+    check(dev, A, B, bias, trans_b=trans_b, label=f"cube{n}")
+
+
+@pytest.mark.parametrize("tile", [128, 256])
+@pytest.mark.parametrize("trans_b", [True, False])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_ragged_tiles_dtypes(dev, tile, trans_b, dtype):
+    M, N, K = 300, 264, 520  # edge tiles in M and N, K tail of 8, vec 8
+    A = oracle.normal(1, (M, K), 0, 1, dtype)
+    B = oracle.normal(2, (N, K) if trans_b else (K, N), 0, 1, dtype)
+    bias = oracle.normal(3, (N,), 0, 1, dtype)
+    check(dev, A, B, bias, trans_b=trans_b, dtype=dtype, tile=tile, label="ragged")
+
+
+@pytest.mark.parametrize("K", [516, 4100, 129, 66])
+def test_k_tails_and_vector_widths(dev, K):
+    # K = 516 / 4100 -> 8-byte loads (vec 4), 129 -> scalar loads, 66 -> scalar; tail tiles partial
+    M, N = 130, 72
+    A = oracle.normal(4, (M, K), 0, 1)
+    B = oracle.normal(5, (N, K), 0, 1)
+    bias = oracle.uniform(6, (N,), -0.5, 0.5)
+    check(dev, A, B, bias, label=f"K{K}")
+    check(dev, A, np.ascontiguousarray(B.T), bias, trans_b=False, label=f"K{K}-nn")
+
+
+@pytest.mark.parametrize("split_k", [2, 4, 7, 16])
+def test_split_k(dev, split_k):
+    M, N, K = 512, 512, 516  # reduced config 2
+    A = oracle.normal(7, (M, K), 0, 1 / np.sqrt(K))
+    B = oracle.normal(8, (N, K), 0, 1 / np.sqrt(K))
+    bias = oracle.uniform(9, (N,), -0.5, 0.5)
+    check(dev, A, B, bias, split_k=split_k, label="splitk")
+
+
+def test_split_k_without_bias_and_odd_n(dev):
+    M, N, K = 77, 61, 700  # N % 8 != 0 -> scalar reduce path
+    A = oracle.normal(10, (M, K), 0, 1)
+    B = oracle.normal(11, (N, K), 0, 1)
+    check(dev, A, B, None, split_k=3, label="splitk-odd")
+
+
+def test_config2_full_size_sampled_rows(dev):
+    # BASELINE config 2 at full size: M=N=4096, K=4100, split-K=4, bias; A,B ~ N(0,1)/sqrt(K),
+    # bias ~ U[-0.5, 0.5). The oracle checks a spread of 96 rows (every output row's kernel path is
+    # the same code; the rows cover several tiles and both edges).
+    M = N = 4096
+    K = 4100
+    A = oracle.normal(1, (M, K), 0, 1 / np.sqrt(K))
+    B = oracle.normal(2, (N, K), 0, 1 / np.sqrt(K))
+    bias = oracle.uniform(3, (N,), -0.5, 0.5)
+    got = mtk.gemm(dev, A, B, bias, split_k=4)
+    rows = np.r_[0:32, 2032:2064, 4064:4096]
+    a = A[rows]
+    exp = oracle.gemm(a, B, bias, trans_b=True)
+    absdot = np.abs(a.astype(np.float64)) @ np.abs(B.astype(np.float64)).T + np.abs(bias.astype(np.float64))
+    res = oracle.compare(got[rows].astype(np.float64), exp, bound=oracle.dot_bound(exp, absdot, K))
+    print(f"[gemm] config2 sampled rows: {res}", flush=True)
+    assert res["ok"], res
+    # the whole output: finite, and split-K 4 agrees with split-K 1 within the same per-element bound
+    got1 = mtk.gemm(dev, A, B, bias, split_k=1)
+    assert np.all(np.isfinite(got.astype(np.float32)))
+    assert oracle.compare(got.astype(np.float64), got1.astype(np.float64), rel_tol=1e-3)["ok"]
+
+
+def test_strided_operands(dev):
+    M, N, K = 96, 80, 200
+    lda, ldb, ldc = 264, 208, 96
+    A = oracle.normal(12, (M, lda), 0, 1)
+    B = oracle.normal(13, (N, ldb), 0, 1)
+    bias = oracle.normal(14, (N,), 0, 1)
+    plan = mtk.GemmPlan(dev, M, N, K, has_bias=True, lda=lda, ldb=ldb, ldc=ldc)
+    dA, dB, db = dev.upload(A), dev.upload(B), dev.upload(bias)
+    dC = dev.upload(np.full((M, ldc), 7.0, np.float16))
+    plan.run(dA, dB, db, dC)
+    dev.sync()
+    C = dev.download(dC, (M, ldc), np.float16)
+    exp = oracle.gemm(np.ascontiguousarray(A[:, :K]), np.ascontiguousarray(B[:, :K]), bias)
+    assert oracle.compare(C[:, :N].astype(np.float64), exp)["ok"]
+    assert np.all(C[:, N:] == 7.0)  # padding columns untouched
+    for b in (dA, dB, db, dC):
+        b.free()
+
+
+def test_run_errors(dev):
+    plan = mtk.GemmPlan(dev, 64, 64, 512, has_bias=True, split_k=2)
+    assert plan.workspace_bytes == 2 * 64 * 64 * 4
+    with pytest.raises(mtk.MtkError):
+        plan.run(0, 0, 0, 0)
+    dA = dev.empty(64 * 512 * 2)
+    with pytest.raises(mtk.MtkError) as e:  # bias promised but missing
+        plan.run(dA, dA, None, dA, dev.empty(plan.workspace_bytes))
+    assert e.value.status == mtk.MTK_ERR_INVALID
+    with pytest.raises(mtk.MtkError) as e:  # split-K plan needs its workspace
+        plan.run(dA, dA, dA, dA, None)
+    assert "workspace" in e.value.message
