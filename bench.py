@@ -1,0 +1,256 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X tensor-op path (BASELINE.json metric), one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
+
+Headline (``value``): BASELINE config 2 -- fp16 GEMM + bias, M = N = 4096, K = 4100, split-K 4,
+B stored [N][K] (the reference's default layout), A, B ~ N(0,1)/sqrt(K), bias ~ U[-0.5, 0.5),
+fp32 accumulate, fp16 out. A step is one run of the path (split-K GEMM + reduce) over resident
+inputs; three input copies rotate so the 256 MB Infinity Cache cannot serve repeats.
+``value`` = 2*M*N*K / (wall time per step), in TFLOP/s.
+
+``roofline`` describes the dominant kernel of the headline step: achieved = algorithmic FLOPs per
+launch / that kernel's average duration (HIP events on the stream it runs on), peak = MI355X's
+published dense fp16 MFMA rate (2.5 PFLOP/s). ``traffic`` comes from the committed rocprofv3
+--pmc FETCH_SIZE / WRITE_SIZE measurement of the same kernel (profiles/traffic.json) when present.
+
+``cpu_baseline``: the CPU oracle (C restatement of matmul.swift:498-510, fp32 sequential
+accumulation, OpenMP over rows) timed on this host on a bounded row sample of the same GEMM.
+
+``configs``: every other BASELINE configuration measured the same way (split-K 1 variant of
+config 2, the bf16 decode GEMM in GB/s, conv2d / conv3d, flash attention fwd both masks).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_F16_TFLOPS = 2500.0  # MI355X published dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_steps(dev, plan, arg_sets, warmup, steps):
+    """Wall time per step over exactly `steps` runs, bracketed by device syncs, plus per-kernel
+    averages from HIP events (mtk_profile) in a second pass."""
+    for i in range(warmup):
+        plan._run(arg_sets[i % len(arg_sets)])
+    dev.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        plan._run(arg_sets[i % len(arg_sets)])
+    dev.sync()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    prof = plan.profile(arg_sets, warmup=1, iters=steps)
+    return wall_ms, prof
+
+
+def gemm_case(dev, mtk, inputs, M, N, K, dtype, split_k, seeds, dists, copies=3, tile=0):
+    plan = mtk.GemmPlan(dev, M, N, K, trans_b=True, dtype=dtype, has_bias=True, split_k=split_k, tile=tile)
+    C = dev.empty(M * N * 2)
+    ws = dev.empty(plan.workspace_bytes) if plan.workspace_bytes else None
+    sets = []
+    for c in range(copies):
+        A = dists[0](inputs, seeds[0] + 100 * c, (M, K), dtype)
+        B = dists[1](inputs, seeds[1] + 100 * c, (N, K), dtype)
+        bias = dists[2](inputs, seeds[2] + 100 * c, (N,), dtype)
+        sets.append(plan.args(dev.upload(A), dev.upload(B), dev.upload(bias), C, ws))
+    return plan, sets
+
+
+def summarize(name, plan, wall_ms, prof, bound):
+    flops, byts = plan.work()
+    kern = max(prof["kernels"].items(), key=lambda kv: kv[1])
+    out = {"workload": name, "plan": plan.describe(), "ms_per_step": wall_ms,
+           "tflops": flops / (wall_ms * 1e-3) / 1e12, "pct_mfma_peak": 100 * flops / (wall_ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS,
+           "kernels_ms": prof["kernels"], "dominant_kernel": kern[0]}
+    if bound == "hbm":
+        out["gbs"] = byts / (wall_ms * 1e-3) / 1e9
+        out["pct_hbm_peak"] = 100 * out["gbs"] / PEAK_HBM_GBS
+        out["kernel_gbs"] = byts / (kern[1] * 1e-3) / 1e9
+    else:
+        out["kernel_tflops"] = flops / (kern[1] * 1e-3) / 1e12
+    return out
+
+
+def cpu_baseline(target_s=10.0):
+    """Oracle GEMM (config 2 shape) on a growing row sample until ~target_s of CPU work."""
+    import oracle
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    M, N, K = 4096, 4096, 4100
+    B = oracle.normal(2, (N, K), 0, 1 / np.sqrt(K))
+    bias = oracle.uniform(3, (N,), -0.5, 0.5)
+    rows, el, reps = 16, 0.0, 1
+    while True:
+        A = oracle.normal(1, (rows, K), 0, 1 / np.sqrt(K))
+        t0 = time.perf_counter()
+        oracle.gemm(A, B, bias, trans_b=True, threads=threads)
+        el = time.perf_counter() - t0
+        if el >= target_s or rows >= M:
+            break
+        rows = min(M, rows * 2 if el < target_s / 4 else int(rows * target_s / max(el, 1e-3)) + 1)
+    if el < target_s:  # whole GEMM done in less than the target: repeat it for a stable time
+        reps = max(1, int(target_s / max(el, 1e-3)))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            oracle.gemm(A, B, bias, trans_b=True, threads=threads)
+        el = (time.perf_counter() - t0) / reps
+    tflops = 2.0 * rows * N * K / el / 1e12
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"oracle_gemm (fp32 sequential accumulate, matmul.swift:498-510) on {rows} of the 4096 rows "
+                      f"of config 2 (M=N=4096, K=4100, bias), {el:.2f} s per run averaged over {reps} run(s), "
+                      f"{threads} threads of {cpu}"}
+
+
+def traffic_for(kernel):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        return t.get(kernel, {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="headline only (no other configs)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs the tensor-op path on a single MI355X and has no "
+              f"multi-GPU mode (asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+
+    import example_matmul_metal4_amd as mtk
+    from example_matmul_metal4_amd import inputs
+
+    dev = mtk.Device(0)
+    info = dev.info
+    log(f"[bench] {info['name']} {info['arch']} CUs={info['compute_units']} clock={info['clock_khz']} kHz "
+        f"computed dense f16 peak={info['peak_f16_tflops']:.1f} TFLOP/s")
+
+    nrm = lambda s: (lambda inp, seed, shape, dt: inp.normal(seed, shape, 0, s, dt))
+    uni = lambda lo, hi: (lambda inp, seed, shape, dt: inp.uniform(seed, shape, lo, hi, dt))
+
+    # ---- headline: config 2
+    M = N = 4096
+    K = 4100
+    plan, sets = gemm_case(dev, mtk, inputs, M, N, K, "f16", 4, (1, 2, 3),
+                           (nrm(1 / np.sqrt(K)), nrm(1 / np.sqrt(K)), uni(-0.5, 0.5)))
+    log(f"[bench] headline plan: {plan.describe()}")
+    wall_ms, prof = time_steps(dev, plan, sets, args.warmup, args.steps)
+    flops, byts = plan.work()
+    value = flops / (wall_ms * 1e-3) / 1e12
+    gemm_kernel = plan.describe().split("kernels:")[1].split()[0]
+    kms = prof["kernels"][gemm_kernel]
+    achieved = flops / (kms * 1e-3) / 1e12
+    log(f"[bench] config2 split-K 4: {wall_ms:.4f} ms/step = {value:.1f} TFLOP/s; kernels {prof['kernels']}")
+
+    line = {
+        "metric": "TFLOP/s + % MFMA peak: fp16 GEMM 4096^3+bias, flash-attn fwd, conv2d, 1 GPU",
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded SplitMix64: A,B ~ N(0,1)/sqrt(K), bias ~ U[-0.5,0.5)); 3 rotating input copies",
+        "config": {"workload": "BASELINE config 2: fp16 GEMM C = A.B^T + bias, M=N=4096, K=4100, split-K=4, "
+                               "B [N][K], fp32 accumulate, fp16 out",
+                   "M": M, "N": N, "K": K, "split_k": 4, "pct_mfma_peak": 100 * value / PEAK_F16_TFLOPS},
+        "roofline": {"bound": "mfma", "kernel": gemm_kernel, "achieved": achieved, "peak": PEAK_F16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic_for(gemm_kernel),
+                     "algorithmic_flops_per_launch": flops, "kernel_ms": kms},
+    }
+
+    # ---- other BASELINE configs (each its own plan, same timing method)
+    if not args.quick:
+        cfgs = {}
+        steps = max(10, args.steps // 2)
+        try:
+            p1, s1 = gemm_case(dev, mtk, inputs, M, N, K, "f16", 1, (1, 2, 3),
+                               (nrm(1 / np.sqrt(K)), nrm(1 / np.sqrt(K)), uni(-0.5, 0.5)))
+            w, pr = time_steps(dev, p1, s1, args.warmup, steps)
+            cfgs["config2_splitk1"] = summarize("config 2 without split-K (split_k=1)", p1, w, pr, "mfma")
+            p3, s3 = gemm_case(dev, mtk, inputs, 16, 14336, 4096, "bf16", 8, (4, 5, 6),
+                               (nrm(1.0), nrm(0.02), nrm(0.02)), copies=3)
+            w, pr = time_steps(dev, p3, s3, args.warmup, steps * 4)
+            cfgs["config3_decode"] = summarize("config 3: bf16 M=16 N=14336 K=4096 split-K 8 + bias (HBM-bound)",
+                                               p3, w, pr, "hbm")
+            for key, dims in (("config4a_conv2d", dict(rank=2, N=8, D=1, H=128, W=128, C=256, O=256, KD=1, KH=3, KW=3,
+                                                       pad_top=1, pad_bottom=1, pad_left=1, pad_right=1)),
+                              ("config4b_conv3d", dict(rank=3, N=1, D=16, H=64, W=64, C=128, O=128, KD=3, KH=3, KW=3,
+                                                       pad_front=1, pad_back=1, pad_top=1, pad_bottom=1, pad_left=1,
+                                                       pad_right=1))):
+                desc = mtk.ConvDesc(stride_d=1, stride_h=1, stride_w=1, dil_d=1, dil_h=1, dil_w=1, has_bias=1,
+                                    dtype=mtk.F16, **dims)
+                pc = mtk.ConvPlan(dev, desc)
+                shape = pc.out_shape()
+                xs = (desc.N, desc.D, desc.H, desc.W, desc.C)
+                ws_ = (desc.KD, desc.KH, desc.KW, desc.C, desc.O)
+                y = dev.empty(int(np.prod(shape)) * 2)
+                sets_c = [pc.args(dev.upload(inputs.uniform(7 + 100 * c, xs, -1, 1)),
+                                  dev.upload(inputs.uniform(8 + 100 * c, ws_, -1, 1)),
+                                  dev.upload(inputs.uniform(9 + 100 * c, (desc.O,), -1, 1)), y) for c in range(3)]
+                w, pr = time_steps(dev, pc, sets_c, args.warmup, steps)
+                cfgs[key] = summarize(pc.describe().split(" kernels:")[0], pc, w, pr, "mfma")
+            for causal in (False, True):
+                pa = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
+                shp = (2, 4096, 32, 128)
+                o = dev.empty(int(np.prod(shp)) * 2)
+                sets_a = [pa.args(dev.upload(inputs.normal(10 + 100 * c, shp)), dev.upload(inputs.normal(11 + 100 * c, shp)),
+                                  dev.upload(inputs.normal(12 + 100 * c, shp)), o) for c in range(2)]
+                w, pr = time_steps(dev, pa, sets_a, args.warmup, steps)
+                s = summarize(f"config 5: flash-attn fwd B=2 H=32 S=4096 D=128 {'causal' if causal else 'non-causal'}",
+                              pa, w, pr, "mfma")
+                s["reference_convention_tflops"] = (2 * 128 + 5) * 4096 * 4096 * 32 * 2 / (
+                    2 if causal else 1) / (w * 1e-3) / 1e12
+                cfgs["config5_attn_causal" if causal else "config5_attn"] = s
+        except Exception as e:  # report what was measured; the headline stands on its own
+            cfgs["error"] = repr(e)
+        line["configs"] = cfgs
+        for k, v in cfgs.items():
+            if isinstance(v, dict):
+                log(f"[bench] {k}: {v.get('ms_per_step', 0):.4f} ms, {v.get('tflops', 0):.1f} TFLOP/s "
+                    f"({v.get('pct_mfma_peak', 0):.1f}% MFMA peak)" + (f", {v['gbs']:.0f} GB/s" if 'gbs' in v else ""))
+
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        log(f"[bench] cpu baseline: {line['cpu_baseline']}")
+    else:
+        line["cpu_baseline"] = None
+    dev.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

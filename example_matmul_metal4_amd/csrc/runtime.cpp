@@ -191,6 +191,48 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   p->gemm = d;
   const char *dt = d.dtype == MTK_F16 ? "f16" : "bf16";
   const int k_tiles = (d.K + 63) / 64;
+  p->flops = 2.0 * d.M * d.N * d.K;
+  p->bytes = 2.0 * ((double)d.M * d.K + (double)d.N * d.K + (double)d.M * d.N + (d.has_bias ? d.N : 0));
+
+  // Decode-shaped problems (M <= 16, B [N][K]) go to the HBM-streaming skinny kernel; its
+  // split-K partitions are wavefronts of one workgroup, reduced on chip with the bias fused.
+  if (d.M <= 16 && d.trans_b && d.tile == 0 && d.K % 8 == 0 && d.lda % 8 == 0 && d.ldb % 8 == 0) {
+    int split = d.split_k == 0 ? (d.K >= 1024 ? 8 : std::max(1, d.K / 128)) : d.split_k;
+    split = std::max(1, std::min(split, 8));
+    int kps = ((d.K + split - 1) / split + 31) / 32 * 32;
+    split = (d.K + kps - 1) / kps;
+    Launch g;
+    g.name = std::string("mtk_skinny_") + dt;
+    g.grid = (unsigned)((d.N + 15) / 16);
+    g.block = (unsigned)(64 * split);
+    mtk_skinny_args a{};
+    a.M = d.M;
+    a.N = d.N;
+    a.K = d.K;
+    a.lda = d.lda;
+    a.ldb = d.ldb;
+    a.ldc = d.ldc;
+    a.a_bytes = (uint32_t)a_bytes;
+    a.b_bytes = (uint32_t)b_bytes;
+    a.split_k = split;
+    a.k_per_split = kps;
+    a.has_bias = d.has_bias ? 1 : 0;
+    set_args(g, a);
+    p->launches.push_back(g);
+    p->align_a = p->align_b = 16;
+    char desc[256];
+    snprintf(desc, sizeof desc,
+             "gemm %s skinny M=%d N=%d K=%d split_k=%d (k/split=%d, reduced in LDS, bias fused) grid=%u block=%u", dt,
+             d.M, d.N, d.K, split, kps, g.grid, g.block);
+    p->description = desc;
+    int s = resolve(p);
+    if (s != MTK_OK) {
+      delete p;
+      return s;
+    }
+    *out = p;
+    return MTK_OK;
+  }
 
   int tile = d.tile;
   int split = d.split_k;
@@ -250,8 +292,6 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
     set_args(r, ra);
     p->launches.push_back(r);
   }
-  p->flops = 2.0 * d.M * d.N * d.K;
-  p->bytes = 2.0 * ((double)d.M * d.K + (double)d.N * d.K + (double)d.M * d.N + (d.has_bias ? d.N : 0));
   char desc[256];
   snprintf(desc, sizeof desc, "gemm %s %s M=%d N=%d K=%d tile=%dx%d split_k=%d k_tiles/split=%d vec=%d grid=%u%s",
            dt, d.trans_b ? "B[N][K]" : "B[K][N]", d.M, d.N, d.K, tile, tile, split, kps, v, g.grid,
@@ -477,6 +517,14 @@ int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
       return fail(MTK_ERR_INVALID, "A/B must be %u-byte aligned for this plan", p->align_a);
     if (p->workspace && (!g->workspace || !aligned(g->workspace, 16)))
       return fail(MTK_ERR_INVALID, "this plan needs a 16-byte aligned workspace of %zu bytes", p->workspace);
+    if (ls[0].name.rfind("mtk_skinny_", 0) == 0) {
+      mtk_skinny_args &k = args_of<mtk_skinny_args>(ls[0]);
+      k.A = g->A;
+      k.B = g->B;
+      k.bias = g->bias;
+      k.C = g->C;
+      return MTK_OK;
+    }
     mtk_tile_args &a = args_of<mtk_tile_args>(ls[0]);
     a.A = g->A;
     a.B = g->B;

@@ -171,3 +171,26 @@ def test_run_errors(dev):
     with pytest.raises(mtk.MtkError) as e:  # split-K plan needs its workspace
         plan.run(dA, dA, dA, dA, None)
     assert "workspace" in e.value.message
+
+
+def test_config3_decode_skinny_full_size(dev):
+    # bf16 M=16, N=14336, K=4096, split-K=8, A ~ N(0,1), B ~ N(0,0.02),
+    # bias ~ N(0,0.02), fp32 accumulate, bf16 out. Every output element is checked.
+    M, N, K = 16, 14336, 4096
+    A = oracle.normal(4, (M, K), 0, 1, "bf16")
+    B = oracle.normal(5, (N, K), 0, 0.02, "bf16")
+    bias = oracle.normal(6, (N,), 0, 0.02, "bf16")
+    plan = mtk.GemmPlan(dev, M, N, K, dtype="bf16", has_bias=True, split_k=8)
+    assert "skinny" in plan.describe() and "split_k=8" in plan.describe()
+    check(dev, A, B, bias, dtype="bf16", split_k=8, label="config3")
+
+
+@pytest.mark.parametrize("M,N,K,split_k,dtype", [
+    (1, 4096, 4096, 8, "bf16"), (3, 100, 1000, 3, "f16"), (16, 64, 128, 1, "f16"), (7, 333, 2048, 2, "bf16"),
+    (16, 14336, 4096, 4, "f16"), (16, 48, 4104, 8, "f16")])
+def test_skinny_shapes(dev, M, N, K, split_k, dtype):
+    A = oracle.normal(20 + M, (M, K), 0, 1, dtype)
+    B = oracle.normal(30 + M, (N, K), 0, 0.05, dtype)
+    bias = oracle.normal(40 + M, (N,), 0, 0.05, dtype)
+    check(dev, A, B, bias, dtype=dtype, split_k=split_k, label="skinny")
+    check(dev, A, B, None, dtype=dtype, split_k=split_k, label="skinny-nobias")
