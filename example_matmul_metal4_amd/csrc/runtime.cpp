@@ -251,12 +251,19 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   const int kps = (k_tiles + split - 1) / split;
   split = (k_tiles + kps - 1) / kps;  // no empty splits
 
-  const int v = d.trans_b ? pow2_vec({d.lda, d.ldb, d.K}) : pow2_vec({d.lda, d.K, d.ldb, d.N});
-  p->align_a = p->align_b = 2 * v;
+  // B [N][K] with 4-byte aligned rows: direct-to-LDS staging (16-byte loads need only dword
+  // alignment; a K tail that is not a multiple of 8 is loaded element-wise). Otherwise the
+  // register-staged kernels with the widest load that divides every leading dimension.
+  const bool direct = d.trans_b && d.lda % 2 == 0 && d.ldb % 2 == 0;
+  const int v = direct ? 8 : (d.trans_b ? pow2_vec({d.lda, d.ldb, d.K}) : pow2_vec({d.lda, d.K, d.ldb, d.N}));
+  p->align_a = p->align_b = direct ? 4 : 2 * v;
 
   Launch g;
   char name[96];
-  snprintf(name, sizeof name, "mtk_gemm_%s_%s_%dx%d_v%d", dt, d.trans_b ? "nt" : "nn", tile, tile, v);
+  if (direct)
+    snprintf(name, sizeof name, "mtk_gemm_%s_nt_%dx%d_d", dt, tile, tile);
+  else
+    snprintf(name, sizeof name, "mtk_gemm_%s_%s_%dx%d_v%d", dt, d.trans_b ? "nt" : "nn", tile, tile, v);
   g.name = name;
   g.grid = (unsigned)(tiles * split);
   mtk_tile_args a{};
@@ -293,8 +300,9 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
     p->launches.push_back(r);
   }
   char desc[256];
-  snprintf(desc, sizeof desc, "gemm %s %s M=%d N=%d K=%d tile=%dx%d split_k=%d k_tiles/split=%d vec=%d grid=%u%s",
-           dt, d.trans_b ? "B[N][K]" : "B[K][N]", d.M, d.N, d.K, tile, tile, split, kps, v, g.grid,
+  snprintf(desc, sizeof desc, "gemm %s %s M=%d N=%d K=%d tile=%dx%d split_k=%d k_tiles/split=%d %s grid=%u%s",
+           dt, d.trans_b ? "B[N][K]" : "B[K][N]", d.M, d.N, d.K, tile, tile, split, kps,
+           direct ? "direct-to-LDS" : (v == 8 ? "vec=8" : v == 4 ? "vec=4" : "vec=1"), g.grid,
            split > 1 ? " + splitk_reduce" : "");
   p->description = desc;
   int s = resolve(p);

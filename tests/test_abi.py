@@ -38,8 +38,9 @@ def test_exports_every_declared_symbol(L):
 def test_code_objects_hold_every_selectable_kernel():
     blobs = b"".join(open(os.path.join(mtk.LIB_DIR, f), "rb").read()
                      for f in os.listdir(mtk.LIB_DIR) if f.endswith(".hsaco"))
-    names = [f"mtk_gemm_{dt}_{lay}_{t}x{t}_v{v}" for dt in ("f16", "bf16") for lay in ("nt", "nn")
-             for t in (128, 256) for v in (8, 4, 1)]
+    names = [f"mtk_gemm_{dt}_nn_{t}x{t}_v{v}" for dt in ("f16", "bf16") for t in (128, 256) for v in (8, 4, 1)]
+    names += [f"mtk_gemm_{dt}_nt_{t}x{t}_v1" for dt in ("f16", "bf16") for t in (128, 256)]
+    names += [f"mtk_gemm_{dt}_nt_{t}x{t}_d" for dt in ("f16", "bf16") for t in (128, 256)]
     names += ["mtk_splitk_reduce_f16", "mtk_splitk_reduce_bf16", "mtk_fill_u16", "mtk_skinny_f16", "mtk_skinny_bf16"]
     names += [f"mtk_attn_fwd_{dt}{c}" for dt in ("f16", "bf16") for c in ("", "_causal")]
     names += [f"mtk_conv_f16_fast_{t}_v{v}" for t in ("256x256", "256x128", "128x128") for v in (8, 4, 1)]
@@ -70,13 +71,15 @@ def test_status_strings(L):
 def test_gemm_kernel_select_dry():
     p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4)
     d = p.describe()
-    assert "mtk_gemm_f16_nt_256x256_v4" in d and "mtk_splitk_reduce_f16" in d and "split_k=4" in d
+    assert "mtk_gemm_f16_nt_256x256_d" in d and "mtk_splitk_reduce_f16" in d and "split_k=4" in d
     assert p.workspace_bytes == 4 * 4096 * 4096 * 4
     flops, byts = p.work()
     assert flops == 2 * 4096 * 4096 * 4100 and byts == 2 * (4096 * 4100 * 2 + 4096 * 4096 + 4096)
     p = mtk.GemmPlan(None, 256, 256, 256, trans_b=False)
     assert "mtk_gemm_f16_nn_128x128_v8" in p.describe() and p.workspace_bytes == 0
     p = mtk.GemmPlan(None, 48, 40, 70, dtype="bf16", trans_b=True)
+    assert "mtk_gemm_bf16_nt_128x128_d" in p.describe()
+    p = mtk.GemmPlan(None, 48, 40, 71, dtype="bf16", trans_b=True)  # odd leading dimension: 2-byte rows
     assert "mtk_gemm_bf16_nt_128x128_v1" in p.describe()
     # the K tail is owned by exactly one split: 65 K-tiles over 4 splits -> 17 per split, 4 splits
     p = mtk.GemmPlan(None, 512, 512, 4100, split_k=4)

@@ -92,7 +92,8 @@ def test_ragged_tiles_dtypes(dev, tile, trans_b, dtype):
 
 @pytest.mark.parametrize("K", [516, 4100, 129, 66])
 def test_k_tails_and_vector_widths(dev, K):
-    # K = 516 / 4100 -> 8-byte loads (vec 4), 129 -> scalar loads, 66 -> scalar; tail tiles partial
+    # B [N][K]: K = 516 / 4100 / 66 -> direct-to-LDS with an element-masked K tail (rows only 4- or
+    # 8-byte aligned); K = 129 -> odd leading dimension, 2-byte scalar loads. B [K][N]: vec 4 / 1.
     M, N = 130, 72
     A = oracle.normal(4, (M, K), 0, 1)
     B = oracle.normal(5, (N, K), 0, 1)
