@@ -295,7 +295,7 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
     ra.has_bias = a.has_bias;
     ra.vec8 = (d.N % 8 == 0 && d.ldc % 8 == 0) ? 1 : 0;
     const long long work = ra.vec8 ? (long long)d.M * d.N / 8 : (long long)d.M * d.N;
-    r.grid = (unsigned)std::min<long long>((work + 255) / 256, 2048);
+    r.grid = (unsigned)std::min<long long>((work + 255) / 256, 65535);
     set_args(r, ra);
     p->launches.push_back(r);
   }
@@ -523,6 +523,7 @@ int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
     if (p->gemm.has_bias && !g->bias) return fail(MTK_ERR_INVALID, "plan has a bias but bias is null");
     if (!aligned(g->A, p->align_a) || !aligned(g->B, p->align_b))
       return fail(MTK_ERR_INVALID, "A/B must be %u-byte aligned for this plan", p->align_a);
+    if (!aligned(g->C, 4)) return fail(MTK_ERR_INVALID, "C must be 4-byte aligned");
     if (p->workspace && (!g->workspace || !aligned(g->workspace, 16)))
       return fail(MTK_ERR_INVALID, "this plan needs a 16-byte aligned workspace of %zu bytes", p->workspace);
     if (ls[0].name.rfind("mtk_skinny_", 0) == 0) {
