@@ -1,32 +1,30 @@
-// fp16 tile-GEMM instantiations: B stored [N][K] ("nt", the reference's default layout) or [K][N]
-// ("nn"), plus the split-K second pass. Kernel names are what the runtime's kernel-select looks up.
-//   *_d    direct-to-LDS staging, B [N][K], operand rows 4-byte aligned
-//   *_vV   register-staged loads V halves wide (8, 4 or 1); for B [N][K] only the 2-byte
-//          path remains (odd leading dimensions), everything else takes *_d
-#include "tile_gemm.hpp"
+// fp16 GEMM instantiations. Kernel names are what the runtime's kernel-select looks up.
+//   *_nt_*_d   B [N][K] (the reference's default layout), direct-to-LDS pipeline
+//   *_nn_*_d   B [K][N] (config 1 "C = A.B row-major"), direct-to-LDS + transposed LDS reads
+//   *_v1       2-byte register-staged fallback for odd leading dimensions
+// plus the split-K second pass.
+#include "tile_direct.hpp"
 
 using namespace mtk;
+
+#define DIRECT_KERNEL(NAME, DT, BM, BN, AOP, BOP)                                   \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const mtk_tile_args a) { \
+    tile_direct<DT, BM, BN, 2, 2, AOP, BOP>(a);                                   \
+  }
 
 #define TILE_KERNEL(NAME, DT, BM, BN, WM, WN, AK, BKIND, VA, VB)                    \
   extern "C" __global__ void __launch_bounds__(256) NAME(const mtk_tile_args a) { \
     tile_gemm<DT, BM, BN, WM, WN, AK, BKIND, VA, VB>(a);                          \
   }
 
-#define DIRECT_KERNEL(NAME, DT, BM, BN, WM, WN)                                   \
-  extern "C" __global__ void __launch_bounds__(256) NAME(const mtk_tile_args a) { \
-    tile_gemm_direct<DT, BM, BN, WM, WN>(a);                                      \
-  }
-
-DIRECT_KERNEL(mtk_gemm_f16_nt_256x256_d, DT_F16, 256, 256, 2, 2)
-DIRECT_KERNEL(mtk_gemm_f16_nt_128x128_d, DT_F16, 128, 128, 2, 2)
+DIRECT_KERNEL(mtk_gemm_f16_nt_256x256_d, DT_F16, 256, 256, OpRows<256>, OpRows<256>)
+DIRECT_KERNEL(mtk_gemm_f16_nt_128x128_d, DT_F16, 128, 128, OpRows<128>, OpRows<128>)
+DIRECT_KERNEL(mtk_gemm_f16_nn_256x256_d, DT_F16, 256, 256, OpRows<256>, OpColsT<256>)
+DIRECT_KERNEL(mtk_gemm_f16_nn_128x128_d, DT_F16, 128, 128, OpRows<128>, OpColsT<128>)
 
 TILE_KERNEL(mtk_gemm_f16_nt_256x256_v1, DT_F16, 256, 256, 2, 2, A_MK, B_NK, 1, 1)
 TILE_KERNEL(mtk_gemm_f16_nt_128x128_v1, DT_F16, 128, 128, 2, 2, A_MK, B_NK, 1, 1)
-TILE_KERNEL(mtk_gemm_f16_nn_256x256_v8, DT_F16, 256, 256, 2, 2, A_MK, B_KN, 8, 8)
-TILE_KERNEL(mtk_gemm_f16_nn_256x256_v4, DT_F16, 256, 256, 2, 2, A_MK, B_KN, 4, 4)
 TILE_KERNEL(mtk_gemm_f16_nn_256x256_v1, DT_F16, 256, 256, 2, 2, A_MK, B_KN, 1, 1)
-TILE_KERNEL(mtk_gemm_f16_nn_128x128_v8, DT_F16, 128, 128, 2, 2, A_MK, B_KN, 8, 8)
-TILE_KERNEL(mtk_gemm_f16_nn_128x128_v4, DT_F16, 128, 128, 2, 2, A_MK, B_KN, 4, 4)
 TILE_KERNEL(mtk_gemm_f16_nn_128x128_v1, DT_F16, 128, 128, 2, 2, A_MK, B_KN, 1, 1)
 
 extern "C" __global__ void __launch_bounds__(256) mtk_splitk_reduce_f16(const mtk_reduce_args a) {

@@ -251,19 +251,16 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   const int kps = (k_tiles + split - 1) / split;
   split = (k_tiles + kps - 1) / kps;  // no empty splits
 
-  // B [N][K] with 4-byte aligned rows: direct-to-LDS staging (16-byte loads need only dword
-  // alignment; a K tail that is not a multiple of 8 is loaded element-wise). Otherwise the
-  // register-staged kernels with the widest load that divides every leading dimension.
-  const bool direct = d.trans_b && d.lda % 2 == 0 && d.ldb % 2 == 0;
-  const int v = direct ? 8 : (d.trans_b ? pow2_vec({d.lda, d.ldb, d.K}) : pow2_vec({d.lda, d.K, d.ldb, d.N}));
-  p->align_a = p->align_b = direct ? 4 : 2 * v;
+  // Operand rows 4-byte aligned (even leading dimensions): the direct-to-LDS pipeline, with B
+  // [N][K] read as row fragments or B [K][N] read through transposed LDS loads (16-byte loads
+  // need only dword alignment; a K tail that is not a multiple of 8 is loaded element-wise).
+  // Odd leading dimensions: the register-staged kernel with 2-byte loads.
+  const bool direct = d.lda % 2 == 0 && d.ldb % 2 == 0;
+  p->align_a = p->align_b = direct ? 4 : 2;
 
   Launch g;
   char name[96];
-  if (direct)
-    snprintf(name, sizeof name, "mtk_gemm_%s_nt_%dx%d_d", dt, tile, tile);
-  else
-    snprintf(name, sizeof name, "mtk_gemm_%s_%s_%dx%d_v%d", dt, d.trans_b ? "nt" : "nn", tile, tile, v);
+  snprintf(name, sizeof name, "mtk_gemm_%s_%s_%dx%d_%s", dt, d.trans_b ? "nt" : "nn", tile, tile, direct ? "d" : "v1");
   g.name = name;
   g.grid = (unsigned)(tiles * split);
   mtk_tile_args a{};
@@ -302,7 +299,7 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   char desc[256];
   snprintf(desc, sizeof desc, "gemm %s %s M=%d N=%d K=%d tile=%dx%d split_k=%d k_tiles/split=%d %s grid=%u%s",
            dt, d.trans_b ? "B[N][K]" : "B[K][N]", d.M, d.N, d.K, tile, tile, split, kps,
-           direct ? "direct-to-LDS" : (v == 8 ? "vec=8" : v == 4 ? "vec=4" : "vec=1"), g.grid,
+           direct ? "direct-to-LDS" : "2-byte loads", g.grid,
            split > 1 ? " + splitk_reduce" : "");
   p->description = desc;
   int s = resolve(p);
@@ -371,14 +368,14 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
   p->ctx = ctx;
   p->kind = PLAN_CONV;
   p->conv = d;
-  const bool fast = (d.C % 64) == 0;
-  int va, vb, bm, bn;
-  const char *kind;
+  // C % 64 == 0 (every 64-wide K-tile is one filter tap), even O and filter extents <= 10: the
+  // direct-to-LDS pipeline (gather with padding as out-of-range loads, weights read transposed).
+  // Anything else: the register-staged generic gather.
+  const bool fast = (d.C % 64) == 0 && d.O % 2 == 0 && d.KD <= 10 && d.KH <= 10 && d.KW <= 10;
+  int va, bm, bn;
   if (fast) {
-    kind = "fast";
     va = 8;
-    vb = pow2_vec({d.O});
-    if (d.O >= 256 || d.O % 256 == 0) {
+    if (d.O >= 256) {
       bm = 256;
       bn = 256;
     } else if (d.O > 64) {
@@ -390,18 +387,18 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
     }
     if ((M + bm - 1) / bm * ((d.O + bn - 1) / bn) < 128) bm = bn = 128;
   } else {
-    kind = "gen";
-    va = vb = pow2_vec({d.C, d.O});
+    va = pow2_vec({d.C, d.O});
     bm = bn = 128;
   }
-  p->align_a = 2 * va;
-  p->align_b = 2 * vb;
+  p->align_a = fast ? 16 : 2 * va;
+  p->align_b = fast ? 4 : 2 * va;
+  const char *kind = fast ? "fast" : "gen";
   Launch g;
   char name[96];
   if (fast)
-    snprintf(name, sizeof name, "mtk_conv_f16_%s_%dx%d_v%d", kind, bm, bn, vb);
+    snprintf(name, sizeof name, "mtk_conv_f16_fast_%dx%d_d", bm, bn);
   else
-    snprintf(name, sizeof name, "mtk_conv_f16_%s_%dx%d_v%d", kind, bm, bn, va);
+    snprintf(name, sizeof name, "mtk_conv_f16_gen_%dx%d_v%d", bm, bn, va);
   g.name = name;
   mtk_tile_args a{};
   a.M = (int)M;

@@ -1,0 +1,430 @@
+// Pipelined MFMA tile kernel with direct-to-LDS staging, parameterised by operand policies.
+//
+// C[M][N] (+ bias) = A . B with A and B given by policies:
+//   A: OpRows  (A [M][lda] row-major, the reference GEMM)            -> LDS [BM][64]
+//      OpConv  (implicit-GEMM gather of an NDHWC activation, C%64==0) -> LDS [BM][64]
+//   B: OpRows  (B [N][ldb], the reference's default transpose.right)  -> LDS [BN][64]
+//      OpColsT (B [K][ldb]: GEMM B [K][N], DHWIO conv weights [K][O])  -> LDS [64][BN]
+//
+// Staging: gfx950 direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds). One wave instruction
+// writes 1 KB of LDS, lane l to byte 16*l; each policy hands every lane the global address of the
+// 16 bytes that belong at that slot, so swizzles are applied on the global side. Out-of-range
+// offsets read as zero and are written to LDS as zero: rows past M/N, the K tail (whole chunks)
+// and convolution padding all cost nothing but an offset select.
+//
+// Fragments: [rows][64] tiles use ds_read_b128 with the chunk swizzle chunk ^ (row&7) ^ ((row>>3)&7);
+// the [64][cols] tile uses two ds_read_b64_tr_b16 per fragment: in each 16-lane group, lane s
+// addresses row k0 + s/4, columns 4*(s%4).. of a 16-column block, and the transposed read hands
+// lane s column s of that block at k0 .. k0+3 — exactly the 32x32x16 MFMA B-operand layout.
+// Chunk swizzle there: chunk ^ 4*(row%4), which spreads the 8 rows one read touches over 16
+// distinct 16-byte bank groups.
+//
+// Pipeline: two LDS stages, one barrier per 64-deep K-tile; each k-step's MFMAs are interleaved in
+// groups with one 1 KB load of the next tile and the next k-step's fragment reads
+// (scheduling fences keep the compiler from regrouping them).
+#pragma once
+
+#include "tile_gemm.hpp"
+
+namespace mtk {
+
+__device__ __forceinline__ void lds_direct16(rsrc_t r, char *lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, off, 0, 0, 0);
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const char *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+
+// Wait for every outstanding LDS read and hand the fragments read by inline asm on to their
+// consumers through this wait: the registers are in/out operands, so no use of them can be
+// scheduled above it.
+template <int N>
+__device__ __forceinline__ void lgkm_wait0(u32x4 (&f)[N]) {
+  if constexpr (N == 1) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]));
+  } else if constexpr (N == 2) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]));
+  } else if constexpr (N == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
+  } else {
+    static_assert(N == 8, "fragment count");
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]),
+                   "+v"(f[7]));
+  }
+}
+
+// ---------------------------------------------------------------- operand policies
+
+// Row-major operand, K contiguous: A [M][lda] or B [N][ldb]. LDS tile [ROWS][64].
+template <int ROWS>
+struct OpRows {
+  static constexpr int kLoads = ROWS / 32;  // 1 KB blocks per wave per K-tile
+  static constexpr bool kNeedsTail = true;  // a K that is not a multiple of 8 needs element masks
+  static constexpr bool kAsmFrag = false;
+  uint32_t off[kLoads];
+  int blk0;
+  int ld;
+
+  __device__ void init(const mtk_tile_args &, int wave, int lane, int row0, int nrows, int ld_) {
+    ld = ld_;
+    blk0 = wave * kLoads;
+    const int cbase = (lane & 7) ^ (lane >> 3);
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int b = blk0 + i, row = row0 + 8 * b + (lane >> 3);
+      off[i] = row < nrows ? (uint32_t)row * (uint32_t)ld * 2u + 16u * (uint32_t)(cbase ^ (b & 7)) : kOOB;
+    }
+  }
+  __device__ __forceinline__ void issue(rsrc_t r, char *lds, int q, int kt) const {
+    lds_direct16(r, lds + (blk0 + q) * 1024, off[q] + (uint32_t)kt * 128u);
+  }
+  // Partial last K-tile: element-masked register loads into the same physical layout.
+  __device__ void tail(rsrc_t r, char *lds, int kt, int K, int lane) const {
+    const int cbase = (lane & 7) ^ (lane >> 3);
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int k = kt * kBK + 8 * (cbase ^ ((blk0 + i) & 7));
+      const uint32_t o = off[i] + (uint32_t)kt * 128u;
+      u32x4 v;
+      if (k >= K) {
+        v = u32x4{};
+      } else if (k + 8 <= K) {
+        v = buf_load16(r, o);
+      } else {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = buf_load2(r, k + e < K ? o + 2u * e : kOOB);
+        v = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+      }
+      *(u32x4 *)(lds + (blk0 + i) * 1024 + lane * 16) = v;
+    }
+  }
+  __device__ __forceinline__ u32x4 frag(const char *lds, int rowblk, int ks, int lane) const {
+    return *(const u32x4 *)(lds + lds_off(rowblk + (lane & 31), 2 * ks + (lane >> 5)));
+  }
+};
+
+// Implicit-GEMM gather of an NDHWC activation (C % 64 == 0, filter extents <= 10): tile row m is
+// output pixel (n, oz, oh, ow); a 64-wide K-tile is one filter tap (kd, kh, kw) and 64 channels.
+// Per tile row the lane keeps the element offset of (n, oz*SZ-PF, oh*SY-PT, ow*SX-PL, 0) plus its
+// chunk, and the in-range taps as three bit masks packed in one word (10 bits each).
+template <int ROWS>
+struct OpConv {
+  static constexpr int kLoads = ROWS / 32;
+  static constexpr bool kNeedsTail = false;  // K = taps * C is a multiple of 64
+  static constexpr bool kAsmFrag = false;
+  int pb8[kLoads];
+  uint32_t pm[kLoads];
+  int blk0;
+
+  __device__ void init(const mtk_tile_args &a, int wave, int lane, int row0, int, int) {
+    blk0 = wave * kLoads;
+    const int cbase = (lane & 7) ^ (lane >> 3);
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int b = blk0 + i;
+      const int m = row0 + 8 * b + (lane >> 3);
+      uint32_t z = 0, h = 0, w = 0;
+      int base = 0;
+      if (m < a.M) {
+        const int ow = m % a.cOW;
+        const int t1 = m / a.cOW;
+        const int oh = t1 % a.cOH;
+        const int t2 = t1 / a.cOH;
+        const int oz = t2 % a.cOD;
+        const int n = t2 / a.cOD;
+        const int iz0 = oz * a.cSZ - a.cPF, ih0 = oh * a.cSY - a.cPT, iw0 = ow * a.cSX - a.cPL;
+        for (int t = 0; t < a.cKD; ++t) z |= (unsigned)(iz0 + t * a.cDZ >= 0 && iz0 + t * a.cDZ < a.cD) << t;
+        for (int t = 0; t < a.cKH; ++t) h |= (unsigned)(ih0 + t * a.cDY >= 0 && ih0 + t * a.cDY < a.cH) << t;
+        for (int t = 0; t < a.cKW; ++t) w |= (unsigned)(iw0 + t * a.cDX >= 0 && iw0 + t * a.cDX < a.cW) << t;
+        base = (((n * a.cD + iz0) * a.cH + ih0) * a.cW + iw0) * a.cC;
+      }
+      pb8[i] = base + 8 * (cbase ^ (b & 7));
+      pm[i] = z | (h << 10) | (w << 20);
+    }
+  }
+  // Tap decode for K-tile kt (uniform across the workgroup).
+  struct Tap {
+    int elems;  // element offset of the tap and the tile's first channel
+    int kd, kh, kw;
+  };
+  __device__ __forceinline__ Tap tap(const mtk_tile_args &a, int kt) const {
+    const int k0 = kt * kBK;
+    const int t = k0 / a.cC;
+    Tap r;
+    r.kw = t % a.cKW;
+    r.kh = (t / a.cKW) % a.cKH;
+    r.kd = t / (a.cKW * a.cKH);
+    r.elems = ((r.kd * a.cDZ * a.cH + r.kh * a.cDY) * a.cW + r.kw * a.cDX) * a.cC + (k0 - t * a.cC);
+    return r;
+  }
+  __device__ __forceinline__ void issue(rsrc_t r, char *lds, int q, const Tap &tp) const {
+    const bool ok = (pm[q] >> tp.kd) & (pm[q] >> (10 + tp.kh)) & (pm[q] >> (20 + tp.kw)) & 1u;
+    lds_direct16(r, lds + (blk0 + q) * 1024, ok ? (uint32_t)(pb8[q] + tp.elems) * 2u : kOOB);
+  }
+  __device__ __forceinline__ u32x4 frag(const char *lds, int rowblk, int ks, int lane) const {
+    return *(const u32x4 *)(lds + lds_off(rowblk + (lane & 31), 2 * ks + (lane >> 5)));
+  }
+};
+
+// [K][ld] operand (N contiguous): GEMM B [K][N], conv weights DHWIO = [K][O]. LDS tile [64][COLS]
+// (row = k), 16-byte chunk c of row k stored at chunk c ^ 4*(k%4).
+template <int COLS>
+struct OpColsT {
+  static constexpr int kRowBytes = COLS * 2;
+  static constexpr int kLoads = COLS / 32;  // 64 rows x kRowBytes / 1 KB / 4 waves
+  static constexpr bool kNeedsTail = false;  // rows k >= K are past the operand: read as zero
+  // Fragment reads are inline asm: the compiler's wait insertion cannot tell the transposed read
+  // builtin apart from the in-flight direct-to-LDS writes of the other stage and would wait for
+  // all of them (vmcnt(0)) before every read. The kernel waits for these reads itself
+  // (frag_wait) before the MFMAs that consume them.
+  static constexpr bool kAsmFrag = true;
+  uint32_t off[kLoads];
+  int blk0;
+  uint32_t kstride;  // bytes per K-tile (64 rows)
+
+  __device__ void init(const mtk_tile_args &, int wave, int lane, int col0, int, int ld) {
+    blk0 = wave * kLoads;
+    kstride = (uint32_t)ld * 2u * kBK;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int byte = (blk0 + i) * 1024 + lane * 16;
+      const int row = byte / kRowBytes;
+      const int pc = (byte % kRowBytes) / 16;
+      const int lc = pc ^ (4 * (row & 3));
+      off[i] = ((uint32_t)row * (uint32_t)ld + (uint32_t)(col0 + 8 * lc)) * 2u;
+    }
+  }
+  __device__ __forceinline__ void issue(rsrc_t r, char *lds, int q, int kt) const {
+    lds_direct16(r, lds + (blk0 + q) * 1024, off[q] + (uint32_t)kt * kstride);
+  }
+  __device__ __forceinline__ u32x4 frag(const char *lds, int colblk, int ks, int lane) const {
+    const int s = lane & 15, h = lane >> 4;
+    const int col = colblk + 16 * (h & 1) + 4 * (s & 3);
+    u32x4 v;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int row = 16 * ks + 8 * (h >> 1) + 4 * e + (s >> 2);
+      const int lc = col >> 3;
+      const char *p = lds + row * kRowBytes + 16 * (lc ^ (4 * (row & 3))) + 2 * (col & 7);
+      u32x2 w;
+      asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(lds_addr(p)));
+      v[2 * e] = w.x;
+      v[2 * e + 1] = w.y;
+    }
+    return v;
+  }
+};
+
+// ---------------------------------------------------------------- the kernel body
+
+template <int DT, int BM, int BN, int WAVES_M, int WAVES_N, typename AOP, typename BOP>
+__device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
+  static_assert(WAVES_M * WAVES_N == 4, "4 wavefronts per workgroup");
+  constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= TN, "fragment reads are paired per row block");
+  constexpr int kStage = (BM + BN) * 128;
+  constexpr int PA = AOP::kLoads, PB = BOP::kLoads;
+  static_assert(PA + PB <= 4 * TM, "one load slot per MFMA group");
+
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_m = wave / WAVES_N, wave_n = wave % WAVES_N;
+
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int split = id / tiles;
+  const int t = id - split * tiles;
+  const int group = kGroupM * a.tiles_n;
+  const int first_m = (t / group) * kGroupM;
+  const int gm = min(a.tiles_m - first_m, kGroupM);
+  const int tm = first_m + (t % group) % gm;
+  const int tn = (t % group) / gm;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kt0 = split * a.k_tiles_per_split;
+  const int kt1 = min(kt0 + a.k_tiles_per_split, a.k_tiles);
+  constexpr bool kAnyTail = AOP::kNeedsTail || BOP::kNeedsTail;
+  static_assert(!AOP::kAsmFrag, "A fragments are read by compiler-visible loads");
+  const bool tail_here = kAnyTail && (a.K % kBK) != 0 && kt1 == a.k_tiles && kt0 < kt1;
+  const int kfull = tail_here ? kt1 - 1 : kt1;
+
+  const rsrc_t ra = make_rsrc(a.A, a.a_bytes);
+  const rsrc_t rb = make_rsrc(a.B, a.b_bytes);
+  AOP opa;
+  BOP opb;
+  opa.init(a, wave, lane, m0, a.M, a.lda);
+  opb.init(a, wave, lane, n0, a.N, a.ldb);
+
+  // one K-tile's loads into stage base `st`
+  auto issue_all = [&](char *st, int kt) {
+    if constexpr (std::is_same<AOP, OpConv<BM>>::value) {
+      const auto tp = opa.tap(a, kt);
+#pragma unroll
+      for (int q = 0; q < PA; ++q) opa.issue(ra, st, q, tp);
+    } else {
+#pragma unroll
+      for (int q = 0; q < PA; ++q) opa.issue(ra, st, q, kt);
+    }
+#pragma unroll
+    for (int q = 0; q < PB; ++q) opb.issue(rb, st + BM * 128, q, kt);
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
+
+  if (kt0 < kfull) issue_all(smem, kt0);
+  wait_vmem();
+  __syncthreads();
+
+  for (int kt = kt0; kt < kfull; ++kt) {
+    const int cur = (kt - kt0) & 1;
+    char *nxt = smem + (cur ^ 1) * kStage;
+    // Branch-free prefetch: on the last full tile this reloads the current tile into the idle
+    // stage (L2 hits, never read) instead of reaching into another split's K range.
+    const int kn = min(kt + 1, kfull - 1);
+    const char *sa = smem + cur * kStage;
+    const char *sb = sa + BM * 128;
+    typename std::conditional<std::is_same<AOP, OpConv<BM>>::value, typename OpConv<BM>::Tap, int>::type tp{};
+    if constexpr (std::is_same<AOP, OpConv<BM>>::value) tp = opa.tap(a, kn);
+
+    u32x4 fa[2][TM], fb[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[0][i] = opa.frag(sa, wave_m * WTM + i * 32, 0, lane);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[0][j] = opb.frag(sb, wave_n * WTN + j * 32, 0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      const int c = ks & 1, nx = c ^ 1;
+      if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[c]);  // this k-step's B fragments (read a step earlier)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa[c][i], fb[c][j], acc[i][j]);
+        const int q = ks * TM + i;
+        if (q < PA) {
+          if constexpr (std::is_same<AOP, OpConv<BM>>::value)
+            opa.issue(ra, nxt, q, tp);
+          else
+            opa.issue(ra, nxt, q, kn);
+        } else if (q < PA + PB) {
+          opb.issue(rb, nxt + BM * 128, q - PA, kn);
+        }
+        if (ks + 1 < kBK / 16) {
+          fa[nx][i] = opa.frag(sa, wave_m * WTM + i * 32, ks + 1, lane);
+          if (i < TN) fb[nx][i] = opb.frag(sb, wave_n * WTN + i * 32, ks + 1, lane);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+  if constexpr (kAnyTail) {
+    if (tail_here) {
+      // the last K-tile of a K that is not a multiple of 64, staged outside the pipeline
+      if constexpr (AOP::kNeedsTail)
+        opa.tail(ra, smem, kfull, a.K, lane);
+      else
+        for (int q = 0; q < PA; ++q) opa.issue(ra, smem, q, kfull);
+      if constexpr (BOP::kNeedsTail)
+        opb.tail(rb, smem + BM * 128, kfull, a.K, lane);
+      else
+        for (int q = 0; q < PB; ++q) opb.issue(rb, smem + BM * 128, q, kfull);
+      wait_vmem();
+      __syncthreads();
+#pragma unroll
+      for (int ks = 0; ks < kBK / 16; ++ks) {
+        u32x4 fa1[TM], fb1[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa1[i] = opa.frag(smem, wave_m * WTM + i * 32, ks, lane);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb1[j] = opb.frag(smem + BM * 128, wave_n * WTN + j * 32, ks, lane);
+        if constexpr (BOP::kAsmFrag) lgkm_wait0(fb1);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa1[i], fb1[j], acc[i][j]);
+      }
+    }
+  }
+
+  // ---- epilogue. 32x32 accumulator layout: lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4,
+  // column l%32 of its block. Adjacent lanes swap one value of each register pair (DPP quad_perm
+  // [1,0,3,2]) so every lane then holds two adjacent columns of one row: even lanes row R, odd
+  // lanes row R+1. Half the store instructions, each 4 bytes (f16/bf16) or 8 bytes (fp32 partial).
+  const bool odd = lane & 1;
+  const int col_l = (lane & 31) & ~1;
+  const int row_l = 4 * (lane >> 5) + (odd ? 1 : 0);
+  const int mw = m0 + wave_m * WTM + row_l, nw = n0 + wave_n * WTN + col_l;
+  auto pair = [&](float x0, float x1, float &lo, float &hi) {
+    const float send = odd ? x0 : x1;
+    const float recv =
+        __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
+    lo = odd ? recv : x0;
+    hi = odd ? x1 : recv;
+  };
+  if (a.partial != nullptr) {
+    float *P = a.partial + (size_t)split * a.M * a.N;
+    const bool vec = (a.N & 1) == 0;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = nw + j * 32;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          float lo, hi;
+          pair(acc[i][j][r], acc[i][j][r + 1], lo, hi);
+          const int row = mw + i * 32 + 8 * (r >> 2) + (r & 3);
+          if (row < a.M) {
+            if (vec && col + 1 < a.N) {
+              *(u32x2 *)(P + (size_t)row * a.N + col) =
+                  u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+            } else {
+              if (col < a.N) P[(size_t)row * a.N + col] = lo;
+              if (col + 1 < a.N) P[(size_t)row * a.N + col + 1] = hi;
+            }
+          }
+        }
+    }
+  } else {
+    uint16_t *C = (uint16_t *)a.C;
+    const uint16_t *bias = (const uint16_t *)a.bias;
+    const bool vec = (a.ldc & 1) == 0;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = nw + j * 32;
+      const int own = col + (odd ? 1 : 0);  // the column this lane's accumulators belong to
+      const float bv = (a.has_bias && own < a.N) ? from_bits<DT>(bias[own]) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          float lo, hi;
+          pair(acc[i][j][r] + bv, acc[i][j][r + 1] + bv, lo, hi);
+          const int row = mw + i * 32 + 8 * (r >> 2) + (r & 3);
+          if (row < a.M) {
+            if (vec && col + 1 < a.N) {
+              *(uint32_t *)(C + (size_t)row * a.ldc + col) = pack2<DT>(lo, hi);
+            } else {
+              if (col < a.N) C[(size_t)row * a.ldc + col] = to_bits<DT>(lo);
+              if (col + 1 < a.N) C[(size_t)row * a.ldc + col + 1] = to_bits<DT>(hi);
+            }
+          }
+        }
+    }
+  }
+}
+
+}  // namespace mtk

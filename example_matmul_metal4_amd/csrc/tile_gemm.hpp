@@ -394,275 +394,7 @@ __device__ __forceinline__ void tile_gemm(const mtk_tile_args &a) {
   }
 }
 
-// ---------------------------------------------------------------- direct-to-LDS variant (B [N][K])
-
-// Row-major operands staged with gfx950 direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds):
-// one wave instruction writes 64 x 16 B = 1 KB = 8 rows of the LDS tile, lane l to byte 16*l of
-// that block, so lane l is given the global chunk that belongs at that physical slot: row
-// 8*blk + l/8, physical chunk l%8, logical chunk (l%8) ^ swizzle(row) = (l%8) ^ (l/8) ^ (blk%8).
-// The lane's byte offset (row start + 16 * logical chunk) is fixed across K-tiles; a K-tile adds
-// kt * 128. No VGPR staging, no ds_write. Only K-tiles entirely below K use it: the last tile of
-// a K that is not a multiple of 64 is staged through registers with element masks (fill_tail).
-// Rows past M / N read zero or keep stale LDS data; either way they only feed accumulator
-// rows / columns that are never stored.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
-
-template <int NBLK>
-__device__ __forceinline__ void direct_issue(rsrc_t r, char *lds, int blk0, const uint32_t *off, int kt) {
-#pragma unroll
-  for (int i = 0; i < NBLK; ++i)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(lds + (blk0 + i) * 1024),
-                                             16, off[i] + (uint32_t)kt * 128u, 0, 0, 0);
-}
-
-template <int NBLK>
-__device__ __forceinline__ void direct_tail(rsrc_t r, char *lds, int blk0, const uint32_t *off, int kt, int K,
-                                            int lane) {
-  const int cbase = (lane & 7) ^ (lane >> 3);
-#pragma unroll
-  for (int i = 0; i < NBLK; ++i) {
-    const int c = cbase ^ ((blk0 + i) & 7);
-    const int k = kt * kBK + 8 * c;
-    const uint32_t o = off[i] + (uint32_t)kt * 128u;
-    u32x4 v;
-    if (k >= K) {
-      v = u32x4{};
-    } else if (k + 8 <= K) {
-      v = buf_load16(r, o);
-    } else {
-      uint32_t h[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = buf_load2(r, k + e < K ? o + 2u * e : kOOB);
-      v = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-    }
-    *(u32x4 *)(lds + (blk0 + i) * 1024 + lane * 16) = v;
-  }
-}
-
-// One 64-deep K-tile on one LDS stage: 4 k-steps of 16. The fragments of step ks+1 are read
-// before the MFMAs of step ks are issued; scheduling fences (sched_barrier) keep the compiler
-// from sinking those reads next to their consumers, so each step's MFMAs run while the next
-// step's LDS reads are in flight (the waits become lgkmcnt(n) for the older group only).
-template <int DT, int TM, int TN, int WTM, int WTN, int NKS = kBK / 16>
-__device__ __forceinline__ void mfma_tile(const char *sa, const char *sb, int wave_m, int wave_n, int frow, int fhalf,
-                                          f32x16 (&acc)[TM][TN]) {
-  u32x4 fa[2][TM], fb[2][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) fa[0][i] = *(const u32x4 *)(sa + lds_off(wave_m * WTM + i * 32 + frow, fhalf));
-#pragma unroll
-  for (int j = 0; j < TN; ++j) fb[0][j] = *(const u32x4 *)(sb + lds_off(wave_n * WTN + j * 32 + frow, fhalf));
-#pragma unroll
-  for (int ks = 0; ks < NKS; ++ks) {
-    const int c = ks & 1, nx = c ^ 1;
-    if (ks + 1 < NKS) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        fa[nx][i] = *(const u32x4 *)(sa + lds_off(wave_m * WTM + i * 32 + frow, 2 * (ks + 1) + fhalf));
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        fb[nx][j] = *(const u32x4 *)(sb + lds_off(wave_n * WTN + j * 32 + frow, 2 * (ks + 1) + fhalf));
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa[c][i], fb[c][j], acc[i][j]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-// The pipelined K-tile: like mfma_tile, but the next tile's global->LDS loads and the next
-// k-step's fragment reads are interleaved with the MFMAs in groups — per k-step, TM groups of
-// [TN MFMAs, one 1 KB direct-to-LDS load, the two fragment reads for row-block i of step ks+1],
-// each group closed by a scheduling fence. Spreading the loads keeps the vector-memory queue
-// from stalling the MFMA issue (measured: 10-12 % faster than issuing all loads up front).
-template <int DT, int TM, int TN, int WTM, int WTN, int PA, int PB>
-__device__ __forceinline__ void mfma_tile_pipelined(const char *sa, const char *sb, char *nxt, int nxt_b_off,
-                                                    rsrc_t ra, rsrc_t rb, const uint32_t *aoff,
-                                                    const uint32_t *boff, int ablk0, int bblk0, int kn,
-                                                    int wave_m, int wave_n, int frow, int fhalf,
-                                                    f32x16 (&acc)[TM][TN]) {
-  static_assert(TM == TN, "square wave tiles");
-  static_assert(PA + PB <= 4 * TM, "one load slot per MFMA group");
-  u32x4 fa[2][TM], fb[2][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) fa[0][i] = *(const u32x4 *)(sa + lds_off(wave_m * WTM + i * 32 + frow, fhalf));
-#pragma unroll
-  for (int j = 0; j < TN; ++j) fb[0][j] = *(const u32x4 *)(sb + lds_off(wave_n * WTN + j * 32 + frow, fhalf));
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int ks = 0; ks < kBK / 16; ++ks) {
-    const int c = ks & 1, nx = c ^ 1;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa[c][i], fb[c][j], acc[i][j]);
-      const int q = ks * TM + i;
-      if (q < PA) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            ra, (__attribute__((address_space(3))) void *)(nxt + (ablk0 + q) * 1024), 16,
-            aoff[q] + (uint32_t)kn * 128u, 0, 0, 0);
-      } else if (q < PA + PB) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rb, (__attribute__((address_space(3))) void *)(nxt + nxt_b_off + (bblk0 + q - PA) * 1024), 16,
-            boff[q - PA] + (uint32_t)kn * 128u, 0, 0, 0);
-      }
-      if (ks + 1 < kBK / 16) {
-        fa[nx][i] = *(const u32x4 *)(sa + lds_off(wave_m * WTM + i * 32 + frow, 2 * (ks + 1) + fhalf));
-        fb[nx][i] = *(const u32x4 *)(sb + lds_off(wave_n * WTN + i * 32 + frow, 2 * (ks + 1) + fhalf));
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-}
-
-template <int DT, int BM, int BN, int WAVES_M, int WAVES_N>
-__device__ __forceinline__ void tile_gemm_direct(const mtk_tile_args &a) {
-  static_assert(WAVES_M * WAVES_N == 4, "4 wavefronts per workgroup");
-  constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
-  constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int kStage = (BM + BN) * 128;
-  constexpr int PA = BM / 32, PB = BN / 32;  // 1 KB blocks per wave per K-tile
-
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wave_m = wave / WAVES_N, wave_n = wave % WAVES_N;
-
-  const int tiles = a.tiles_m * a.tiles_n;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int split = id / tiles;
-  const int t = id - split * tiles;
-  const int group = kGroupM * a.tiles_n;
-  const int first_m = (t / group) * kGroupM;
-  const int gm = min(a.tiles_m - first_m, kGroupM);
-  const int tm = first_m + (t % group) % gm;
-  const int tn = (t % group) / gm;
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int kt0 = split * a.k_tiles_per_split;
-  const int kt1 = min(kt0 + a.k_tiles_per_split, a.k_tiles);
-  // the partial last K-tile (if any) is peeled off the pipelined loop
-  const bool tail_here = (a.K % kBK) != 0 && kt1 == a.k_tiles && kt0 < kt1;
-  const int kfull = tail_here ? kt1 - 1 : kt1;
-
-  const rsrc_t ra = make_rsrc(a.A, a.a_bytes);
-  const rsrc_t rb = make_rsrc(a.B, a.b_bytes);
-  const int cbase = (lane & 7) ^ (lane >> 3);
-  const int ablk0 = wave * PA, bblk0 = wave * PB;
-  uint32_t aoff[PA], boff[PB];
-#pragma unroll
-  for (int i = 0; i < PA; ++i) {
-    const int b = ablk0 + i, row = m0 + 8 * b + (lane >> 3);
-    aoff[i] = row < a.M ? (uint32_t)row * (uint32_t)a.lda * 2u + 16u * (uint32_t)(cbase ^ (b & 7)) : kOOB;
-  }
-#pragma unroll
-  for (int i = 0; i < PB; ++i) {
-    const int b = bblk0 + i, row = n0 + 8 * b + (lane >> 3);
-    boff[i] = row < a.N ? (uint32_t)row * (uint32_t)a.ldb * 2u + 16u * (uint32_t)(cbase ^ (b & 7)) : kOOB;
-  }
-
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
-
-  const int frow = lane & 31;
-  const int fhalf = lane >> 5;
-
-  if (kt0 < kfull) {
-    direct_issue<PA>(ra, smem, ablk0, aoff, kt0);
-    direct_issue<PB>(rb, smem + BM * 128, bblk0, boff, kt0);
-  }
-  wait_vmem();
-  __syncthreads();
-
-  for (int kt = kt0; kt < kfull; ++kt) {
-    const int cur = (kt - kt0) & 1;
-    char *nxt = smem + (cur ^ 1) * kStage;
-    // Branch-free prefetch: on the last full tile this reloads the current tile into the idle
-    // stage (L2 hits, never read) instead of reaching into another split's K range.
-    const int kn = min(kt + 1, kfull - 1);
-    const char *sa = smem + cur * kStage;
-    mfma_tile_pipelined<DT, TM, TN, WTM, WTN, PA, PB>(sa, sa + BM * 128, nxt, BM * 128, ra, rb, aoff, boff, ablk0,
-                                                      bblk0, kn, wave_m, wave_n, frow, fhalf, acc);
-    wait_vmem();
-    __syncthreads();
-  }
-  if (tail_here) {
-    direct_tail<PA>(ra, smem, ablk0, aoff, kfull, a.K, lane);
-    direct_tail<PB>(rb, smem + BM * 128, bblk0, boff, kfull, a.K, lane);
-    __syncthreads();
-    mfma_tile<DT, TM, TN, WTM, WTN>(smem, smem + BM * 128, wave_m, wave_n, frow, fhalf, acc);
-  }
-
-  // ---- epilogue. 32x32 accumulator layout: lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4,
-  // column l%32 of its block. Adjacent lanes swap one value of each register pair (DPP quad_perm
-  // [1,0,3,2]) so every lane then holds two adjacent columns of one row: even lanes row R, odd
-  // lanes row R+1. Half the store instructions, each 4 bytes (f16/bf16) or 8 bytes (fp32 partial).
-  const bool odd = lane & 1;
-  const int col_l = (lane & 31) & ~1;
-  const int row_l = 4 * (lane >> 5) + (odd ? 1 : 0);
-  const int mw = m0 + wave_m * WTM + row_l, nw = n0 + wave_n * WTN + col_l;
-  auto pair = [&](float x0, float x1, float &lo, float &hi) {
-    const float send = odd ? x0 : x1;
-    const float recv = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
-    lo = odd ? recv : x0;
-    hi = odd ? x1 : recv;
-  };
-  if (a.partial != nullptr) {
-    float *P = a.partial + (size_t)split * a.M * a.N;
-    const bool vec = (a.N & 1) == 0;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = nw + j * 32;
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          float lo, hi;
-          pair(acc[i][j][r], acc[i][j][r + 1], lo, hi);
-          const int row = mw + i * 32 + 8 * (r >> 2) + (r & 3);
-          if (row < a.M) {
-            if (vec && col + 1 < a.N) {
-              *(u32x2 *)(P + (size_t)row * a.N + col) = u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
-            } else {
-              if (col < a.N) P[(size_t)row * a.N + col] = lo;
-              if (col + 1 < a.N) P[(size_t)row * a.N + col + 1] = hi;
-            }
-          }
-        }
-    }
-  } else {
-    uint16_t *C = (uint16_t *)a.C;
-    const uint16_t *bias = (const uint16_t *)a.bias;
-    const bool vec = (a.ldc & 1) == 0;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = nw + j * 32;
-      const int own = col + (odd ? 1 : 0);  // the column this lane's accumulators belong to
-      const float bv = (a.has_bias && own < a.N) ? from_bits<DT>(bias[own]) : 0.0f;
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          float lo, hi;
-          pair(acc[i][j][r] + bv, acc[i][j][r + 1] + bv, lo, hi);
-          const int row = mw + i * 32 + 8 * (r >> 2) + (r & 3);
-          if (row < a.M) {
-            if (vec && col + 1 < a.N) {
-              *(uint32_t *)(C + (size_t)row * a.ldc + col) = pack2<DT>(lo, hi);
-            } else {
-              if (col < a.N) C[(size_t)row * a.ldc + col] = to_bits<DT>(lo);
-              if (col + 1 < a.N) C[(size_t)row * a.ldc + col + 1] = to_bits<DT>(hi);
-            }
-          }
-        }
-    }
-  }
-}
 
 // Second pass of split-K: C[m][n] = (sum over splits, in order) + bias[n], rounded once.
 // HBM-bound: reads the split_k fp32 partials once and writes C once. A thread owns 8 consecutive

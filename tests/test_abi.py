@@ -38,12 +38,11 @@ def test_exports_every_declared_symbol(L):
 def test_code_objects_hold_every_selectable_kernel():
     blobs = b"".join(open(os.path.join(mtk.LIB_DIR, f), "rb").read()
                      for f in os.listdir(mtk.LIB_DIR) if f.endswith(".hsaco"))
-    names = [f"mtk_gemm_{dt}_nn_{t}x{t}_v{v}" for dt in ("f16", "bf16") for t in (128, 256) for v in (8, 4, 1)]
-    names += [f"mtk_gemm_{dt}_nt_{t}x{t}_v1" for dt in ("f16", "bf16") for t in (128, 256)]
-    names += [f"mtk_gemm_{dt}_nt_{t}x{t}_d" for dt in ("f16", "bf16") for t in (128, 256)]
+    names = [f"mtk_gemm_{dt}_{lay}_{t}x{t}_{v}" for dt in ("f16", "bf16") for lay in ("nt", "nn") for t in (128, 256)
+             for v in ("d", "v1")]
     names += ["mtk_splitk_reduce_f16", "mtk_splitk_reduce_bf16", "mtk_fill_u16", "mtk_skinny_f16", "mtk_skinny_bf16"]
     names += [f"mtk_attn_fwd_{dt}{c}" for dt in ("f16", "bf16") for c in ("", "_causal")]
-    names += [f"mtk_conv_f16_fast_{t}_v{v}" for t in ("256x256", "256x128", "128x128") for v in (8, 4, 1)]
+    names += [f"mtk_conv_f16_fast_{t}_d" for t in ("256x256", "256x128", "128x128")]
     names += [f"mtk_conv_f16_gen_128x128_v{v}" for v in (8, 4, 1)]
     missing = [n for n in names if n.encode() not in blobs]
     assert not missing, missing
@@ -76,7 +75,7 @@ def test_gemm_kernel_select_dry():
     flops, byts = p.work()
     assert flops == 2 * 4096 * 4096 * 4100 and byts == 2 * (4096 * 4100 * 2 + 4096 * 4096 + 4096)
     p = mtk.GemmPlan(None, 256, 256, 256, trans_b=False)
-    assert "mtk_gemm_f16_nn_128x128_v8" in p.describe() and p.workspace_bytes == 0
+    assert "mtk_gemm_f16_nn_128x128_d" in p.describe() and p.workspace_bytes == 0
     p = mtk.GemmPlan(None, 48, 40, 70, dtype="bf16", trans_b=True)
     assert "mtk_gemm_bf16_nt_128x128_d" in p.describe()
     p = mtk.GemmPlan(None, 48, 40, 71, dtype="bf16", trans_b=True)  # odd leading dimension: 2-byte rows
@@ -126,12 +125,12 @@ def test_dry_plan_refuses_to_run():
 def test_conv_kernel_select_and_shapes():
     d = oracle.ConvDims.conv2d(N=8, H=128, W=128, C=256, O=256, PT=1, PB=1, PL=1, PR=1)
     p = mtk.ConvPlan(None, mtk.conv_desc(d, has_bias=True))
-    assert "mtk_conv_f16_fast_256x256_v8" in p.describe()
+    assert "mtk_conv_f16_fast_256x256_d" in p.describe()
     assert p.out_shape() == (8, 128, 128, 256)
     assert p.work()[0] == d.flops() == 154618822656
     d3 = oracle.ConvDims.conv3d(N=1, D=16, H=64, W=64, C=128, O=128, PF=1, PBk=1, PT=1, PB=1, PL=1, PR=1)
     p = mtk.ConvPlan(None, mtk.conv_desc(d3))
-    assert "mtk_conv_f16_fast_256x128_v8" in p.describe() and p.out_shape() == (1, 16, 64, 64, 128)
+    assert "mtk_conv_f16_fast_256x128_d" in p.describe() and p.out_shape() == (1, 16, 64, 64, 128)
     assert p.work()[0] == d3.flops() == 57982058496
     # the reference's case lists: every output shape agrees with the oracle's formulas
     import json
