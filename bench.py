@@ -69,12 +69,13 @@ def gemm_case(dev, mtk, inputs, M, N, K, dtype, split_k, seeds, dists, copies=3,
     return plan, sets
 
 
-def summarize(name, plan, wall_ms, prof, bound):
+def summarize(name, plan, wall_ms, prof, bound, key=None):
     flops, byts = plan.work()
     kern = max(prof["kernels"].items(), key=lambda kv: kv[1])
     out = {"workload": name, "plan": plan.describe(), "ms_per_step": wall_ms,
            "tflops": flops / (wall_ms * 1e-3) / 1e12, "pct_mfma_peak": 100 * flops / (wall_ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS,
-           "kernels_ms": prof["kernels"], "dominant_kernel": kern[0]}
+           "kernels_ms": prof["kernels"], "dominant_kernel": kern[0],
+           "traffic": traffic_for(f"{kern[0]}@{key}") if key else None}
     if bound == "hbm":
         out["gbs"] = byts / (wall_ms * 1e-3) / 1e9
         out["pct_hbm_peak"] = 100 * out["gbs"] / PEAK_HBM_GBS
@@ -122,12 +123,14 @@ def cpu_baseline(target_s=10.0):
                       f"{threads} threads of {cpu}"}
 
 
-def traffic_for(kernel):
+def traffic_for(key):
+    """HBM bytes per launch of kernel@workload from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    measurement (profiles/traffic.json, copy-calibrated), or None."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
             t = json.load(f)
-        return t.get(kernel, {}).get("hbm_bytes_per_launch")
+        return t.get(key, {}).get("hbm_bytes_per_launch")
     except (OSError, ValueError):
         return None
 
@@ -166,7 +169,7 @@ def main():
     wall_ms, prof = time_steps(dev, plan, sets, args.warmup, args.steps)
     flops, byts = plan.work()
     value = flops / (wall_ms * 1e-3) / 1e12
-    gemm_kernel = plan.describe().split("kernels:")[1].split()[0]
+    gemm_kernel = next(k for k in plan.describe().split("kernels:")[1].split() if k.startswith("mtk_gemm_"))
     kms = prof["kernels"][gemm_kernel]
     achieved = flops / (kms * 1e-3) / 1e12
     log(f"[bench] config2 split-K 4: {wall_ms:.4f} ms/step = {value:.1f} TFLOP/s; kernels {prof['kernels']}")
@@ -188,7 +191,7 @@ def main():
                                "B [N][K], fp32 accumulate, fp16 out",
                    "M": M, "N": N, "K": K, "split_k": 4, "pct_mfma_peak": 100 * value / PEAK_F16_TFLOPS},
         "roofline": {"bound": "mfma", "kernel": gemm_kernel, "achieved": achieved, "peak": PEAK_F16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic_for(gemm_kernel),
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic_for(f"{gemm_kernel}@config2_splitk4"),
                      "algorithmic_flops_per_launch": flops, "kernel_ms": kms},
     }
 
@@ -200,12 +203,13 @@ def main():
             p1, s1 = gemm_case(dev, mtk, inputs, M, N, K, "f16", 1, (1, 2, 3),
                                (nrm(1 / np.sqrt(K)), nrm(1 / np.sqrt(K)), uni(-0.5, 0.5)))
             w, pr = time_steps(dev, p1, s1, args.warmup, steps)
-            cfgs["config2_splitk1"] = summarize("config 2 without split-K (split_k=1)", p1, w, pr, "mfma")
+            cfgs["config2_splitk1"] = summarize("config 2 without split-K (split_k=1)", p1, w, pr, "mfma",
+                                                key="config2_splitk1")
             p3, s3 = gemm_case(dev, mtk, inputs, 16, 14336, 4096, "bf16", 8, (4, 5, 6),
                                (nrm(1.0), nrm(0.02), nrm(0.02)), copies=3)
             w, pr = time_steps(dev, p3, s3, args.warmup, steps * 4)
             cfgs["config3_decode"] = summarize("config 3: bf16 M=16 N=14336 K=4096 split-K 8 + bias (HBM-bound)",
-                                               p3, w, pr, "hbm")
+                                               p3, w, pr, "hbm", key="config3_decode")
             for key, dims in (("config4a_conv2d", dict(rank=2, N=8, D=1, H=128, W=128, C=256, O=256, KD=1, KH=3, KW=3,
                                                        pad_top=1, pad_bottom=1, pad_left=1, pad_right=1)),
                               ("config4b_conv3d", dict(rank=3, N=1, D=16, H=64, W=64, C=128, O=128, KD=3, KH=3, KW=3,
@@ -222,7 +226,7 @@ def main():
                                   dev.upload(inputs.uniform(8 + 100 * c, ws_, -1, 1)),
                                   dev.upload(inputs.uniform(9 + 100 * c, (desc.O,), -1, 1)), y) for c in range(3)]
                 w, pr = time_steps(dev, pc, sets_c, args.warmup, steps)
-                cfgs[key] = summarize(pc.describe().split(" kernels:")[0], pc, w, pr, "mfma")
+                cfgs[key] = summarize(pc.describe().split(" kernels:")[0], pc, w, pr, "mfma", key=key)
             for causal in (False, True):
                 pa = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
                 shp = (2, 4096, 32, 128)
@@ -231,7 +235,7 @@ def main():
                                   dev.upload(inputs.normal(12 + 100 * c, shp)), o) for c in range(2)]
                 w, pr = time_steps(dev, pa, sets_a, args.warmup, steps)
                 s = summarize(f"config 5: flash-attn fwd B=2 H=32 S=4096 D=128 {'causal' if causal else 'non-causal'}",
-                              pa, w, pr, "mfma")
+                              pa, w, pr, "mfma", key="config5_causal" if causal else "config5")
                 s["reference_convention_tflops"] = (2 * 128 + 5) * 4096 * 4096 * 32 * 2 / (
                     2 if causal else 1) / (w * 1e-3) / 1e12
                 cfgs["config5_attn_causal" if causal else "config5_attn"] = s

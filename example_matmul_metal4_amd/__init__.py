@@ -288,6 +288,10 @@ class _Plan:
     def _run(self, args):
         _check(getattr(lib(), self._run_fn)(self.handle, ctypes.byref(args)))
 
+    def launch(self, args):
+        """Enqueue one run with prepared arguments (from ``args(...)``) on the context's stream."""
+        self._run(args)
+
     def profile(self, arg_sets, warmup: int = 2, iters: int = 10) -> dict:
         """ProfileOptions{warmupIterations, timedIterations}: per-kernel average ms over ``iters``."""
         arr = (self._args_type * len(arg_sets))(*arg_sets)

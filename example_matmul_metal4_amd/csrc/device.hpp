@@ -12,12 +12,17 @@ namespace mtk {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Note: __builtin_bit_cast applied directly to a vector element (v.y, w[2]) reads element 0 with
+// this compiler (ROCm 7.2 clang); copy the element to a scalar first or load a vector of the
+// wanted element type.
 
 enum { DT_F16 = 0, DT_BF16 = 1 };
 

@@ -9,7 +9,7 @@
 
 #include <stdint.h>
 
-#define MTK_KARGS_VERSION 1
+#define MTK_KARGS_VERSION 2
 
 /* Tile-GEMM kernels: plain GEMM (A [M][K] . B, B either [N][K] or [K][N]) and
  * implicit-GEMM convolution (A = im2col of an NDHWC activation, B = DHWIO
@@ -47,6 +47,13 @@ typedef struct {
   int32_t has_bias;
   int32_t vec8; /* 1: N, ldc multiple of 8 and C, bias 16-byte aligned -> 8-wide path */
 } mtk_reduce_args;
+
+/* 16-bit fill (zeroing workspaces inside a plan; graph-capturable, unlike hipMemsetAsync). */
+typedef struct {
+  void *p;
+  uint64_t n; /* elements */
+  uint32_t v;
+} mtk_fill_args;
 
 /* Skinny (decode-shaped) GEMM: A [M <= 16][lda], B [N][ldb] (NK), fp32 partials per K split. */
 typedef struct {

@@ -80,10 +80,13 @@ namespace {
 
 enum PlanKind { PLAN_GEMM = 1, PLAN_ATTN = 2, PLAN_CONV = 3 };
 
+enum LaunchRole { ROLE_MAIN = 0, ROLE_REDUCE = 1 };
+
 struct Launch {
   std::string name;
   hipFunction_t fn = nullptr;
   unsigned grid = 1, block = 256;
+  LaunchRole role = ROLE_MAIN;
   std::vector<char> args;  // kernel argument block (one struct, by value)
 };
 
@@ -283,6 +286,7 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   if (split > 1) {
     p->workspace = (size_t)split * d.M * d.N * sizeof(float);
     Launch r;
+    r.role = ROLE_REDUCE;
     r.name = std::string("mtk_splitk_reduce_") + dt;
     mtk_reduce_args ra{};
     ra.M = d.M;
@@ -531,21 +535,22 @@ int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
       k.C = g->C;
       return MTK_OK;
     }
-    mtk_tile_args &a = args_of<mtk_tile_args>(ls[0]);
-    a.A = g->A;
-    a.B = g->B;
-    a.bias = g->bias;
-    if (ls.size() > 1) {
-      a.C = nullptr;
-      a.partial = (float *)g->workspace;
-      mtk_reduce_args &r = args_of<mtk_reduce_args>(ls[1]);
-      r.partial = (const float *)g->workspace;
-      r.bias = g->bias;
-      r.C = g->C;
-      r.vec8 = r.vec8 && aligned(g->C, 16) && (!g->bias || aligned(g->bias, 16));
-    } else {
-      a.C = g->C;
-      a.partial = nullptr;
+    const bool split = p->workspace != 0;
+    for (Launch &l : ls) {
+      if (l.role == ROLE_MAIN) {
+        mtk_tile_args &a = args_of<mtk_tile_args>(l);
+        a.A = g->A;
+        a.B = g->B;
+        a.bias = g->bias;
+        a.C = split ? nullptr : g->C;
+        a.partial = split ? (float *)g->workspace : nullptr;
+      } else if (l.role == ROLE_REDUCE) {
+        mtk_reduce_args &r = args_of<mtk_reduce_args>(l);
+        r.partial = (const float *)g->workspace;
+        r.bias = g->bias;
+        r.C = g->C;
+        r.vec8 = r.vec8 && aligned(g->C, 16) && (!g->bias || aligned(g->bias, 16));
+      }
     }
   } else if (p->kind == PLAN_CONV) {
     const mtk_conv_args *c = (const mtk_conv_args *)argset;
@@ -767,11 +772,7 @@ int mtk_fill_u16(mtk_ctx *ctx, void *dst, uint16_t value, size_t count) {
   hipFunction_t f;
   int s = ctx->function("mtk_fill_u16", &f);
   if (s != MTK_OK) return s;
-  struct {
-    void *p;
-    uint64_t n;
-    uint32_t v;
-  } a{dst, count, value};
+  mtk_fill_args a{dst, (uint64_t)count, value};
   void *params[] = {&a};
   unsigned grid = (unsigned)std::min<size_t>((count + 255) / 256, 4096);
   HIP_TRY(hipSetDevice(ctx->device));

@@ -26,6 +26,10 @@
 
 #include "tile_gemm.hpp"
 
+#ifndef MTK_LOAD_GROUPS
+#define MTK_LOAD_GROUPS 8
+#endif
+
 namespace mtk {
 
 __device__ __forceinline__ void lds_direct16(rsrc_t r, char *lds, uint32_t off) {
@@ -229,7 +233,11 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   static_assert(TM >= TN, "fragment reads are paired per row block");
   constexpr int kStage = (BM + BN) * 128;
   constexpr int PA = AOP::kLoads, PB = BOP::kLoads;
-  static_assert(PA + PB <= 4 * TM, "one load slot per MFMA group");
+  // The next K-tile's loads go out in the first kLoadGroups MFMA groups of the current one, so
+  // they have most of the tile's MFMA time to land before the end-of-tile wait.
+  constexpr int kGroups = (kBK / 16) * TM;
+  constexpr int kLoadGroups = MTK_LOAD_GROUPS < kGroups ? MTK_LOAD_GROUPS : kGroups;
+  constexpr int kPerGroup = (PA + PB + kLoadGroups - 1) / kLoadGroups;
 
   __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
 
@@ -311,14 +319,17 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       for (int i = 0; i < TM; ++i) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa[c][i], fb[c][j], acc[i][j]);
-        const int q = ks * TM + i;
-        if (q < PA) {
-          if constexpr (std::is_same<AOP, OpConv<BM>>::value)
-            opa.issue(ra, nxt, q, tp);
-          else
-            opa.issue(ra, nxt, q, kn);
-        } else if (q < PA + PB) {
-          opb.issue(rb, nxt + BM * 128, q - PA, kn);
+#pragma unroll
+        for (int u = 0; u < kPerGroup; ++u) {
+          const int q = (ks * TM + i) * kPerGroup + u;
+          if (q < PA) {
+            if constexpr (std::is_same<AOP, OpConv<BM>>::value)
+              opa.issue(ra, nxt, q, tp);
+            else
+              opa.issue(ra, nxt, q, kn);
+          } else if (q < PA + PB) {
+            opb.issue(rb, nxt + BM * 128, q - PA, kn);
+          }
         }
         if (ks + 1 < kBK / 16) {
           fa[nx][i] = opa.frag(sa, wave_m * WTM + i * 32, ks + 1, lane);
@@ -374,7 +385,9 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     lo = odd ? recv : x0;
     hi = odd ? x1 : recv;
   };
-  if (a.partial != nullptr) {
+  // Split-K partials: GEMM only (convolution plans never split K).
+  constexpr bool kPartials = !std::is_same<AOP, OpConv<BM>>::value;
+  if (kPartials && a.partial != nullptr) {
     float *P = a.partial + (size_t)split * a.M * a.N;
     const bool vec = (a.N & 1) == 0;
 #pragma unroll
@@ -388,12 +401,12 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
           pair(acc[i][j][r], acc[i][j][r + 1], lo, hi);
           const int row = mw + i * 32 + 8 * (r >> 2) + (r & 3);
           if (row < a.M) {
+            // partials are streamed out once and read once by the second pass: non-temporal
             if (vec && col + 1 < a.N) {
-              *(u32x2 *)(P + (size_t)row * a.N + col) =
-                  u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+              __builtin_nontemporal_store(f32x2{lo, hi}, (f32x2 *)(P + (size_t)row * a.N + col));
             } else {
-              if (col < a.N) P[(size_t)row * a.N + col] = lo;
-              if (col + 1 < a.N) P[(size_t)row * a.N + col + 1] = hi;
+              if (col < a.N) __builtin_nontemporal_store(lo, P + (size_t)row * a.N + col);
+              if (col + 1 < a.N) __builtin_nontemporal_store(hi, P + (size_t)row * a.N + col + 1);
             }
           }
         }

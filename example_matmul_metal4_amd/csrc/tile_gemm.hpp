@@ -410,10 +410,12 @@ __device__ __forceinline__ void splitk_reduce(const mtk_reduce_args &a) {
     for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups; g += (size_t)gridDim.x * blockDim.x) {
       const size_t e = g * 8;
       const int m = (int)(e / a.N), n = (int)(e % a.N);
-      f32x4 s0 = *(const f32x4 *)(a.partial + e), s1 = *(const f32x4 *)(a.partial + e + 4);
+      // partials are read exactly once: non-temporal loads
+      f32x4 s0 = __builtin_nontemporal_load((const f32x4 *)(a.partial + e));
+      f32x4 s1 = __builtin_nontemporal_load((const f32x4 *)(a.partial + e + 4));
       for (int s = 1; s < a.split_k; ++s) {
-        s0 += *(const f32x4 *)(a.partial + s * plane + e);
-        s1 += *(const f32x4 *)(a.partial + s * plane + e + 4);
+        s0 += __builtin_nontemporal_load((const f32x4 *)(a.partial + s * plane + e));
+        s1 += __builtin_nontemporal_load((const f32x4 *)(a.partial + s * plane + e + 4));
       }
       if (a.has_bias) {
         const u32x4 b = *(const u32x4 *)(bias + n);

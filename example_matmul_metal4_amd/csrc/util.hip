@@ -2,13 +2,7 @@
 // capture it in a HIP graph).
 #include "device.hpp"
 
-struct FillArgs {
-  void *p;
-  uint64_t n;
-  uint32_t v;
-};
-
-extern "C" __global__ void __launch_bounds__(256) mtk_fill_u16(const FillArgs a) {
+extern "C" __global__ void __launch_bounds__(256) mtk_fill_u16(const mtk_fill_args a) {
   uint16_t *p = (uint16_t *)a.p;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += (uint64_t)gridDim.x * blockDim.x)
     p[i] = (uint16_t)a.v;

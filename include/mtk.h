@@ -101,9 +101,9 @@ int mtk_set_stream(mtk_ctx *ctx, void *hip_stream);
  *   B: trans_b != 0 -> [N][ldb] (the reference default, createSource(transpose: (false, true)),
  *      matmul.swift:366); trans_b == 0 -> [K][ldb]
  *   C: [M][ldc] row-major; bias: [N] (same dtype) or NULL.
- * split_k: 1 = none; >1 = that many K partitions with fp32 partials reduced by a second pass
- * with the bias fused (the reference's reduce_sum_2, matmul.swift:298-311, 451-474, without its
- * in-place race); 0 = let the plan choose.
+ * split_k: 1 = none; >1 = that many K partitions with fp32 partials, summed in partition order
+ * with the bias added last (the reference's reduce_sum_2, matmul.swift:298-311, 451-474, without
+ * its in-place race); 0 = let the plan choose.
  * tile: 0 = let the plan choose; else 128 or 256 (square MFMA workgroup tile). */
 typedef struct {
   int M, N, K;
