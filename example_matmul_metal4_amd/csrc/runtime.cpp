@@ -198,15 +198,19 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   p->bytes = 2.0 * ((double)d.M * d.K + (double)d.N * d.K + (double)d.M * d.N + (d.has_bias ? d.N : 0));
 
   // Decode-shaped problems (M <= 16, B [N][K]) go to the HBM-streaming skinny kernel; its
-  // split-K partitions are wavefronts of one workgroup, reduced on chip with the bias fused.
+  // split-K partitions are wavefronts of one workgroup, reduced on chip with the bias fused. The
+  // grid is persistent: one workgroup per CU walking the 16-column groups.
   if (d.M <= 16 && d.trans_b && d.tile == 0 && d.K % 8 == 0 && d.lda % 8 == 0 && d.ldb % 8 == 0) {
     int split = d.split_k == 0 ? (d.K >= 1024 ? 8 : std::max(1, d.K / 128)) : d.split_k;
     split = std::max(1, std::min(split, 8));
     int kps = ((d.K + split - 1) / split + 31) / 32 * 32;
     split = (d.K + kps - 1) / kps;
+    const long long groups = (d.N + 15) / 16;
+    const int cus = ctx ? ctx->prop.multiProcessorCount : 256;
     Launch g;
-    g.name = std::string("mtk_skinny_") + dt;
-    g.grid = (unsigned)((d.N + 15) / 16);
+    // partitions of up to 512 K keep their A fragments in registers for the whole kernel
+    g.name = std::string("mtk_skinny_") + dt + (kps <= 512 ? "" : "_long");
+    g.grid = (unsigned)std::min<long long>(groups, cus);
     g.block = (unsigned)(64 * split);
     mtk_skinny_args a{};
     a.M = d.M;

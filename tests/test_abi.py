@@ -40,7 +40,8 @@ def test_code_objects_hold_every_selectable_kernel():
                      for f in os.listdir(mtk.LIB_DIR) if f.endswith(".hsaco"))
     names = [f"mtk_gemm_{dt}_{lay}_{t}x{t}_{v}" for dt in ("f16", "bf16") for lay in ("nt", "nn") for t in (128, 256)
              for v in ("d", "v1")]
-    names += ["mtk_splitk_reduce_f16", "mtk_splitk_reduce_bf16", "mtk_fill_u16", "mtk_skinny_f16", "mtk_skinny_bf16"]
+    names += ["mtk_splitk_reduce_f16", "mtk_splitk_reduce_bf16", "mtk_fill_u16", "mtk_skinny_f16", "mtk_skinny_bf16",
+              "mtk_skinny_f16_long", "mtk_skinny_bf16_long"]
     names += [f"mtk_attn_fwd_{dt}{c}" for dt in ("f16", "bf16") for c in ("", "_causal")]
     names += [f"mtk_conv_f16_fast_{t}_d" for t in ("256x256", "256x128", "128x128")]
     names += [f"mtk_conv_f16_gen_128x128_v{v}" for v in (8, 4, 1)]
@@ -87,6 +88,10 @@ def test_gemm_kernel_select_dry():
     p = mtk.GemmPlan(None, 16, 14336, 4096, dtype="bf16", has_bias=True, split_k=8)
     assert "mtk_skinny_bf16" in p.describe() and "split_k=8" in p.describe() and p.workspace_bytes == 0
     assert "mtk_skinny_f16" not in mtk.GemmPlan(None, 17, 64, 64).describe()
+    # partitions longer than 512 K reload A per pass; the grid is persistent (<= one workgroup per CU)
+    p = mtk.GemmPlan(None, 8, 14336, 8192, split_k=4)
+    assert "mtk_skinny_f16_long" in p.describe() and "grid=256 " in p.describe()
+    assert "grid=3 " in mtk.GemmPlan(None, 8, 40, 256, split_k=2).describe()
     # split-K never produces an empty split
     p = mtk.GemmPlan(None, 64, 64, 100, split_k=8)
     assert "split_k=2 k_tiles/split=1" in p.describe()
