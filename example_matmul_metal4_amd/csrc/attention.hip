@@ -6,21 +6,26 @@
 // with a batch dimension). Extensions: batch, causal mask (keys j <= i + S_kv - S_q), bf16.
 //
 // Work decomposition
-//   * Workgroup = 4 wavefronts = 128 query rows of one (batch, head); each wave owns 32 queries.
-//     K/V are streamed in tiles of 64 keys through two LDS stages (one barrier per tile).
-//   * Scores are computed transposed, S^T = K . Q^T, on 32x32x16 MFMA: the accumulator column
-//     (lane % 32) is the query, so each lane owns one query and the softmax row max / row sum are
-//     in-register reductions plus one exchange with lane ^ 32.
+//   * Workgroup = 4 wavefronts = 128 query rows of one (batch, head); each wave owns 32 queries,
+//     held in registers as the B operand of S^T = K . Q^T. K and V stream through LDS in tiles of
+//     64 keys, two LDS slots each, filled by direct-to-LDS loads (no register staging).
+//   * Scores are computed transposed on 32x32x16 MFMA: the accumulator column (lane % 32) is the
+//     query, so each lane owns one query and the softmax row max / row sum are in-register
+//     reductions plus one exchange with lane ^ 32.
 //   * K rows are fed to the MFMA in a permuted order (MFMA row m reads key swap_bits_2_3(m)); with
 //     that order accumulator register r of lane (i, g = lane/32) holds key 8g + r (r < 8) or
-//     16 + 8g + (r - 8), which is exactly the B-operand layout of the P.V MFMA
-//     (O^T = V^T . P^T). P therefore goes from the S accumulators to the next MFMA with only an
-//     fp32 -> 16-bit conversion, never through LDS.
-//   * V is transposed while staging to LDS (4x8 register transposes), so V^T fragments are
-//     single 16-byte LDS reads. K rows (256 B) use a chunk ^ (row & 15) swizzle, V^T rows (128 B)
-//     chunk ^ (row & 7) ^ ((row >> 3) & 7); both keep the fragment reads bank-conflict free.
-//   * O is rescaled only when some lane's running max moved (wave-uniform branch).
-//   * Global reads are raw buffer loads: rows past S (ragged tails) read zero, never fault.
+//     16 + 8g + (r - 8), which is exactly the B-operand layout of the P.V MFMA (O^T = V^T . P^T).
+//     P goes from the S accumulators to the next MFMA with only an fp32 -> 16-bit conversion.
+//   * V stays [key][d] in LDS; the V^T operand is read with transposed LDS reads
+//     (ds_read_b64_tr_b16, two per fragment). K rows (256 B) use a chunk ^ (row & 15) swizzle,
+//     V rows chunk ^ 4 * (row & 3): both keep the fragment reads free of bank conflicts.
+//   * Software pipeline across key tiles, in one wavefront's instruction stream: the MFMAs of
+//     S(t+1) are interleaved with the exponentials of softmax(t), and the P(t).V(t) MFMAs with the
+//     row maxima of S(t+1), so the matrix cores and the vector ALUs work at the same time.
+//   * Lazy rescale: the exponent offset of a query moves only when its running max exceeds it by
+//     more than 8 (log2 domain), so P <= 2^8 (exact in fp16/bf16 range) and O is rescaled on few
+//     tiles; 1/l at the end makes the result independent of the offsets.
+//   * Global reads are raw buffer loads: keys past S_kv and queries past S_q read zero.
 //   * Causal: a workgroup stops at its last visible key tile; heavy query blocks are dispatched
 //     first; query blocks of one (batch, head) are kept on one XCD for K/V reuse in L2.
 #include "device.hpp"
@@ -30,28 +35,22 @@ namespace mtk {
 constexpr int kD = 128;
 constexpr int kBQ = 128;
 constexpr int kBKV = 64;
-constexpr int kStageBytes = 2 * kBKV * kD * 2;  // K tile + V^T tile
+constexpr int kTile = kBKV * kD * 2;   // bytes of one K or V tile in LDS
+constexpr float kRescaleSlack = 8.0f;  // log2-domain headroom before O is rescaled
 
 __device__ __forceinline__ int swap_bits_2_3(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
-__device__ __forceinline__ uint32_t k_off(int row, int chunk) {  // 64 rows x 256 B
+__device__ __forceinline__ uint32_t k_off(int row, int chunk) {  // K tile: 64 rows x 256 B
   return (uint32_t)(row * 256 + ((chunk ^ (row & 15)) << 4));
-}
-__device__ __forceinline__ uint32_t vt_off(int d, int chunk) {  // 128 rows x 128 B
-  return (uint32_t)(kBKV * kD * 2 + d * 128 + ((chunk ^ (d & 7) ^ ((d >> 3) & 7)) << 4));
-}
-
-template <int DT>
-__device__ __forceinline__ uint32_t half_of(const u32x4 &v, int e) {  // 16-bit element e of 8
-  const uint32_t w = v[e >> 1];
-  return (e & 1) ? (w >> 16) : (w & 0xffffu);
 }
 
 template <int DT, bool CAUSAL>
 __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * kStageBytes];
+  // K slots 0, 1 then V slots 0, 1
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTile];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, col = lane & 31;
 
   const int id = xcd_remap(blockIdx.x, gridDim.x);
@@ -79,127 +78,177 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
   if (CAUSAL) kv_end = min(a.S_kv, q0 + kBQ + diag);
   const int n_tiles = kv_end > 0 ? (kv_end + kBKV - 1) / kBKV : 0;
 
-  // ---- staging: K as 4 chunks per thread, V as a 4-key x 8-dim block per thread
-  const int kchunk = tid & 15;
-  const int vjq = tid >> 4, vdb = tid & 15;
-  u32x4 kr[4], vr[4];
-  auto load_kv = [&](int t) {
-    const int j0 = t * kBKV;
+  // ---- direct-to-LDS staging: each wave fills 4 KB of a tile (4 rows of 256 B per instruction).
+  // K: LDS chunk pc of row r holds global chunk pc ^ (r & 15); V: pc ^ 4 * (r & 3).
+  int srow[4];
+  uint32_t kcol[4], vcol[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    srow[i] = (wave * 4 + i) * 4 + (lane >> 4);
+    const int pc = lane & 15;
+    kcol[i] = 16u * (uint32_t)(pc ^ (srow[i] & 15));
+    vcol[i] = 16u * (uint32_t)(pc ^ (4 * (srow[i] & 3)));
+  }
+  auto issue_k = [&](int slot, int t) {
+    char *dst = smem + slot * kTile + wave * 4096;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int key = j0 + (tid >> 4) + 16 * i;
-      kr[i] = buf_load16(rk, key < a.S_kv ? kvbase + (uint32_t)key * rs + (uint32_t)kchunk * 16u : kOOB);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = j0 + 4 * vjq + i;
-      vr[i] = buf_load16(rv, key < a.S_kv ? kvbase + (uint32_t)key * rs + (uint32_t)vdb * 16u : kOOB);
+      const int key = t * kBKV + srow[i];
+      lds_direct16(rk, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + kcol[i] : kOOB);
     }
   };
-  auto store_kv = [&](int s) {
-    char *st = smem + s * kStageBytes;
+  auto issue_v = [&](int slot, int t) {
+    char *dst = smem + (2 + slot) * kTile + wave * 4096;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *(u32x4 *)(st + k_off((tid >> 4) + 16 * i, kchunk)) = kr[i];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = vdb * 8 + e;
-      const uint32_t lo = half_of<DT>(vr[0], e) | (half_of<DT>(vr[1], e) << 16);
-      const uint32_t hi = half_of<DT>(vr[2], e) | (half_of<DT>(vr[3], e) << 16);
-      *(u32x2 *)(st + vt_off(d, vjq >> 1) + (vjq & 1) * 8) = u32x2{lo, hi};
+    for (int i = 0; i < 4; ++i) {
+      const int key = t * kBKV + srow[i];
+      lds_direct16(rv, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + vcol[i] : kOOB);
     }
   };
 
-  float m_run = -1e30f;  // running max of scaled logits (log2 domain)
-  float l_run = 0.0f;    // this lane's half of the running row sum
+  // ---- fragment reads
+  const int krow = swap_bits_2_3(col);
+  auto kfrag = [&](const char *kt, int blk, int ds) -> u32x4 {
+    return *(const u32x4 *)(kt + k_off(krow + 32 * blk, 2 * ds + g));
+  };
+  // V^T fragment for d block db, key step js (16 keys): lane (h = lane / 16, s = lane % 16) gets
+  // d = 32 db + lane % 32 at keys 16 js + 8 (lane / 32) + 0..7.
+  const int vs = lane & 15, vh = lane >> 4;
+  auto vfrag = [&](const char *vt, int db, int js) -> u32x4 {
+    const int d = 32 * db + 16 * (vh & 1) + 4 * (vs & 3);
+    u32x4 v;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int row = 16 * js + 8 * (vh >> 1) + 4 * e + (vs >> 2);
+      const u32x2 w = ds_read_tr16(vt + row * 256 + 16 * ((d >> 3) ^ (4 * (row & 3))) + 2 * (d & 7));
+      v[2 * e] = w.x;
+      v[2 * e + 1] = w.y;
+    }
+    return v;
+  };
+
+  float m_off = -INFINITY;  // exponent offset of this lane's query (log2 domain)
+  float l_run = 0.0f;       // this lane's half of the running row sum
   f32x16 o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = f32x16{};
-
-  const int krow = swap_bits_2_3(col);
   const float c = a.scale_log2;
   const int wave_q_min = q0 + wave * 32;
 
   if (n_tiles > 0) {
-    load_kv(0);
-    store_kv(0);
-  }
-  __syncthreads();
-
-  for (int t = 0; t < n_tiles; ++t) {
-    const int cur = t & 1;
-    const bool more = t + 1 < n_tiles;
-    if (more) load_kv(t + 1);
-    const char *st = smem + cur * kStageBytes;
-
-    // S^T for 64 keys: two 32-key blocks
-    f32x16 s0 = f32x16{}, s1 = f32x16{};
+    f32x16 s0 = f32x16{}, s1 = f32x16{};  // S^T of the tile being softmaxed
+    issue_k(0, 0);
+    wait_vmem();
+    __syncthreads();
+    if (n_tiles > 1) issue_k(1, 1);
+    issue_v(0, 0);
+    {
+      const char *kt = smem;
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) {
-      const int ch = 2 * ds + g;
-      const u32x4 k0 = *(const u32x4 *)(st + k_off(krow, ch));
-      const u32x4 k1 = *(const u32x4 *)(st + k_off(krow + 32, ch));
-      s0 = mfma32x32x16<DT>(k0, qf[ds], s0);
-      s1 = mfma32x32x16<DT>(k1, qf[ds], s1);
-    }
-
-    const int j0 = t * kBKV;
-    const bool need_mask = (j0 + kBKV > a.S_kv) || (CAUSAL && j0 + kBKV - 1 > wave_q_min + diag);
-    if (need_mask) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kr0 = (r < 8) ? (8 * g + r) : (16 + 8 * g + (r - 8));
-        const int key0 = j0 + kr0, key1 = j0 + 32 + kr0;
-        const bool v0 = key0 < a.S_kv && (!CAUSAL || key0 <= qi + diag);
-        const bool v1 = key1 < a.S_kv && (!CAUSAL || key1 <= qi + diag);
-        s0[r] = v0 ? s0[r] : -INFINITY;
-        s1[r] = v1 ? s1[r] : -INFINITY;
+      for (int ds = 0; ds < 8; ++ds) {
+        s0 = mfma32x32x16<DT>(kfrag(kt, 0, ds), qf[ds], s0);
+        s1 = mfma32x32x16<DT>(kfrag(kt, 1, ds), qf[ds], s1);
       }
     }
-
-    // online softmax (base 2)
+    // row max of tile 0
     float mx = fmaxf(s0[0], s1[0]);
 #pragma unroll
     for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx * c);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-    float psum = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c, -m_new));
-      s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], c, -m_new));
-      psum += s0[r] + s1[r];
-    }
-    l_run = l_run * alpha + psum;
-    if (__any(alpha != 1.0f)) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] *= alpha;
-    }
 
-    // P^T as the B operand, 16 keys per MFMA k-step: js = 2 * block + half
-    u32x4 pf[4];
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      pf[hf] = u32x4{pack2<DT>(s0[8 * hf + 0], s0[8 * hf + 1]), pack2<DT>(s0[8 * hf + 2], s0[8 * hf + 3]),
-                     pack2<DT>(s0[8 * hf + 4], s0[8 * hf + 5]), pack2<DT>(s0[8 * hf + 6], s0[8 * hf + 7])};
-      pf[2 + hf] = u32x4{pack2<DT>(s1[8 * hf + 0], s1[8 * hf + 1]), pack2<DT>(s1[8 * hf + 2], s1[8 * hf + 3]),
-                         pack2<DT>(s1[8 * hf + 4], s1[8 * hf + 5]), pack2<DT>(s1[8 * hf + 6], s1[8 * hf + 7])};
-    }
+    for (int t = 0; t < n_tiles; ++t) {
+      wait_vmem();
+      __syncthreads();  // K(t+1) and V(t) are in LDS; K slot t&1 and V slot (t+1)&1 are free
+      // (on the last tile, S(t+1) is computed from whatever the K slot holds and discarded)
+      if (t + 2 < n_tiles) issue_k(t & 1, t + 2);
+      if (t + 1 < n_tiles) issue_v((t + 1) & 1, t + 1);
+      const char *kn = smem + ((t + 1) & 1) * kTile;
+      const char *vt = smem + (2 + (t & 1)) * kTile;
 
-    // O^T += V^T . P^T
+      // mask of tile t (only tiles crossing S_kv or the causal diagonal)
+      const int j0 = t * kBKV;
+      if ((j0 + kBKV > a.S_kv) || (CAUSAL && j0 + kBKV - 1 > wave_q_min + diag)) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const int vrow = db * 32 + col;
+        for (int r = 0; r < 16; ++r) {
+          const int kr0 = (r < 8) ? (8 * g + r) : (16 + 8 * g + (r - 8));
+          const int key0 = j0 + kr0, key1 = j0 + 32 + kr0;
+          s0[r] = (key0 < a.S_kv && (!CAUSAL || key0 <= qi + diag)) ? s0[r] : -INFINITY;
+          s1[r] = (key1 < a.S_kv && (!CAUSAL || key1 <= qi + diag)) ? s1[r] : -INFINITY;
+        }
+        mx = fmaxf(s0[0], s1[0]);
 #pragma unroll
-      for (int js = 0; js < 4; ++js) {
-        const u32x4 vf = *(const u32x4 *)(st + vt_off(vrow, 2 * js + g));
-        o[db] = mfma32x32x16<DT>(vf, pf[js], o[db]);
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
       }
-    }
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_tile = mx * c;
+      float alpha = 1.0f;
+      if (m_tile > m_off + kRescaleSlack) {
+        alpha = __builtin_amdgcn_exp2f(m_off - m_tile);
+        m_off = m_tile;
+      }
+      const float moff = m_off == -INFINITY ? 0.0f : m_off;  // fully masked so far: P = 0
+      // rescale here, not after phase A: a branch between the MFMAs and the exponentials would let
+      // the compiler sink the exponentials past it and lose the interleave
+      l_run *= alpha;
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] *= alpha;
+      }
 
-    if (more) store_kv(cur ^ 1);
-    __syncthreads();
+      // phase A: S(t+1) MFMAs interleaved with exp / sum / pack of tile t
+      f32x16 n0 = f32x16{}, n1 = f32x16{};
+      u32x4 pf[4];
+      float psum = 0.0f;
+#pragma unroll
+      for (int ds = 0; ds < 8; ++ds) {
+        n0 = mfma32x32x16<DT>(kfrag(kn, 0, ds), qf[ds], n0);
+        n1 = mfma32x32x16<DT>(kfrag(kn, 1, ds), qf[ds], n1);
+        // 4 of the 32 scores per step: registers 2*ds, 2*ds+1 of both blocks
+        const int r = 2 * ds;
+        const float p00 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c, -moff));
+        const float p01 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r + 1], c, -moff));
+        const float p10 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], c, -moff));
+        const float p11 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r + 1], c, -moff));
+        psum += (p00 + p01) + (p10 + p11);
+        // registers 0..7 -> keys 0..15 of the block (P k-step 2*blk), 8..15 -> keys 16..31
+        pf[r >> 3][(r & 7) >> 1] = pack2<DT>(p00, p01);
+        pf[2 + (r >> 3)][(r & 7) >> 1] = pack2<DT>(p10, p11);
+      }
+      // machine-scheduler pattern for phase A: each MFMA followed by one K fragment read and a
+      // share of the softmax VALU work
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // first two K fragment reads
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        if (i < 14) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // next K fragment read
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      l_run += psum;
+
+      // phase B: O^T += V^T(t) . P^T(t), interleaved with the row max of S(t+1); the next d
+      // block's V^T fragments are read while the current block's MFMAs run
+      u32x4 vf[2][4];
+#pragma unroll
+      for (int js = 0; js < 4; ++js) vf[0][js] = vfrag(vt, 0, js);
+      float mn = fmaxf(n0[0], n1[0]);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int cb = db & 1, nb = cb ^ 1;
+        lgkm_wait0(vf[cb]);
+        if (db + 1 < 4) {
+#pragma unroll
+          for (int js = 0; js < 4; ++js) vf[nb][js] = vfrag(vt, db + 1, js);
+        }
+#pragma unroll
+        for (int js = 0; js < 4; ++js) o[db] = mfma32x32x16<DT>(vf[cb][js], pf[js], o[db]);
+#pragma unroll
+        for (int r = 4 * db; r < 4 * db + 4; ++r) mn = fmaxf(mn, fmaxf(n0[r], n1[r]));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      s0 = n0;
+      s1 = n1;
+      mx = mn;
+    }
   }
 
   // ---- epilogue: O[qi][h][d] = O^T[d][qi] / l
@@ -231,6 +280,6 @@ using namespace mtk;
   }
 
 ATTN_KERNEL(mtk_attn_fwd_f16, DT_F16, false)
-ATTN_KERNEL(mtk_attn_fwd_f16_causal, DT_F16, true)
 ATTN_KERNEL(mtk_attn_fwd_bf16, DT_BF16, false)
+ATTN_KERNEL(mtk_attn_fwd_f16_causal, DT_F16, true)
 ATTN_KERNEL(mtk_attn_fwd_bf16_causal, DT_BF16, true)

@@ -101,6 +101,52 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 __device__ __forceinline__ uint32_t pack_lo(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x05040100u); }
 __device__ __forceinline__ uint32_t pack_hi(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
 
+// ---------------------------------------------------------------- LDS staging and reads
+
+// gfx950 direct-to-LDS load (buffer_load_dwordx4 ... lds): lane l of the wave writes the 16 bytes
+// at buffer offset `off` to LDS byte lds + 16 * l (one instruction fills 1 KB). Out-of-range
+// offsets write zeros.
+__device__ __forceinline__ void lds_direct16(rsrc_t r, char *lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, off, 0, 0, 0);
+}
+
+// Wait until every vector-memory load of this wave has completed, direct-to-LDS ones included.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const char *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+
+// ds_read_b64_tr_b16 as inline asm. The compiler's wait insertion cannot tell the transposed-read
+// builtin apart from in-flight direct-to-LDS writes and would wait for all of them (vmcnt(0))
+// before every read; callers of this form wait for the read themselves with lgkm_wait0.
+// In each 16-lane group, lane s addresses row k0 + s/4, columns 4*(s%4) .. of a 16-column block of
+// 16-bit elements; lane s receives column s of that block at rows k0 .. k0+3.
+__device__ __forceinline__ u32x2 ds_read_tr16(const char *p) {
+  u32x2 w;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(lds_addr(p)));
+  return w;
+}
+
+// Wait for every outstanding LDS read and hand registers filled by inline-asm reads on to their
+// consumers through this wait: they are in/out operands, so no use can be scheduled above it.
+template <int N>
+__device__ __forceinline__ void lgkm_wait0(u32x4 (&f)[N]) {
+  if constexpr (N == 1) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]));
+  } else if constexpr (N == 2) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]));
+  } else if constexpr (N == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
+  } else {
+    static_assert(N == 8, "fragment count");
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]),
+                   "+v"(f[7]));
+  }
+}
+
 // Workgroup id remap so that consecutive logical ids share an XCD: hardware hands
 // workgroup b to XCD (b % 8); XCD x receives its ids in order, so logical id =
 // (ids owned by XCDs before x) + (b / 8). A bijection on [0, n).

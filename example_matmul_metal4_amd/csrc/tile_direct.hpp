@@ -32,34 +32,6 @@
 
 namespace mtk {
 
-__device__ __forceinline__ void lds_direct16(rsrc_t r, char *lds, uint32_t off) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, off, 0, 0, 0);
-}
-
-// LDS byte address of a pointer into a __shared__ array.
-__device__ __forceinline__ uint32_t lds_addr(const char *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
-}
-
-// Wait for every outstanding LDS read and hand the fragments read by inline asm on to their
-// consumers through this wait: the registers are in/out operands, so no use of them can be
-// scheduled above it.
-template <int N>
-__device__ __forceinline__ void lgkm_wait0(u32x4 (&f)[N]) {
-  if constexpr (N == 1) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]));
-  } else if constexpr (N == 2) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]));
-  } else if constexpr (N == 4) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
-  } else {
-    static_assert(N == 8, "fragment count");
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]),
-                   "+v"(f[7]));
-  }
-}
-
 // ---------------------------------------------------------------- operand policies
 
 // Row-major operand, K contiguous: A [M][lda] or B [N][ldb]. LDS tile [ROWS][64].
@@ -214,8 +186,7 @@ struct OpColsT {
       const int row = 16 * ks + 8 * (h >> 1) + 4 * e + (s >> 2);
       const int lc = col >> 3;
       const char *p = lds + row * kRowBytes + 16 * (lc ^ (4 * (row & 3))) + 2 * (col & 7);
-      u32x2 w;
-      asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(lds_addr(p)));
+      const u32x2 w = ds_read_tr16(p);
       v[2 * e] = w.x;
       v[2 * e + 1] = w.y;
     }

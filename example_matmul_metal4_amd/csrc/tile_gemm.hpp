@@ -394,12 +394,11 @@ __device__ __forceinline__ void tile_gemm(const mtk_tile_args &a) {
   }
 }
 
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
-
 // Second pass of split-K: C[m][n] = (sum over splits, in order) + bias[n], rounded once.
 // HBM-bound: reads the split_k fp32 partials once and writes C once. A thread owns 8 consecutive
 // outputs (two 16-byte loads per split); the grid covers the whole output in one pass (measured
-// best on MI355X: 6.9 TB/s standalone; wider per-thread work and non-temporal loads were slower).
+// on MI355X: about 5-7 TB/s; wider per-thread work was slower). The partials are written and read
+// non-temporally: they are streamed once each way.
 template <int DT>
 __device__ __forceinline__ void splitk_reduce(const mtk_reduce_args &a) {
   const uint16_t *bias = (const uint16_t *)a.bias;
