@@ -207,7 +207,8 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   // The next K-tile's loads go out in the first kLoadGroups MFMA groups of the current one, so
   // they have most of the tile's MFMA time to land before the end-of-tile wait.
   constexpr int kGroups = (kBK / 16) * TM;
-  constexpr int kLoadGroups = MTK_LOAD_GROUPS < kGroups ? MTK_LOAD_GROUPS : kGroups;
+  // every load of the next K-tile is issued before the last k-step, where the barrier waits for it
+  constexpr int kLoadGroups = MTK_LOAD_GROUPS < kGroups - TM ? MTK_LOAD_GROUPS : kGroups - TM;
   constexpr int kPerGroup = (PA + PB + kLoadGroups - 1) / kLoadGroups;
 
   __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
@@ -265,6 +266,15 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   wait_vmem();
   __syncthreads();
 
+  // Fragments of the first k-step of the first tile. Afterwards the last k-step of every tile
+  // reads the next tile's first fragments: the barrier sits before that k-step (its own fragments
+  // are already in registers), so its MFMAs cover the latency of those reads.
+  u32x4 fa[2][TM], fb[2][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) fa[0][i] = opa.frag(smem, wave_m * WTM + i * 32, 0, lane);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) fb[0][j] = opb.frag(smem + BM * 128, wave_n * WTN + j * 32, 0, lane);
+
   for (int kt = kt0; kt < kfull; ++kt) {
     const int cur = (kt - kt0) & 1;
     char *nxt = smem + (cur ^ 1) * kStage;
@@ -275,17 +285,21 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     const char *sb = sa + BM * 128;
     typename std::conditional<std::is_same<AOP, OpConv<BM>>::value, typename OpConv<BM>::Tap, int>::type tp{};
     if constexpr (std::is_same<AOP, OpConv<BM>>::value) tp = opa.tap(a, kn);
-
-    u32x4 fa[2][TM], fb[2][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) fa[0][i] = opa.frag(sa, wave_m * WTM + i * 32, 0, lane);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) fb[0][j] = opb.frag(sb, wave_n * WTN + j * 32, 0, lane);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
       const int c = ks & 1, nx = c ^ 1;
+      constexpr int kLast = kBK / 16 - 1;
+      if (ks == kLast) {
+        // the next tile has landed (own loads: vmcnt; everyone's: barrier) and every wave is done
+        // reading this tile's stage, which the next iteration starts to overwrite
+        wait_vmem();
+        __syncthreads();
+      }
       if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[c]);  // this k-step's B fragments (read a step earlier)
+      const char *ra_ = ks < kLast ? sa : nxt;
+      const char *rb_ = ks < kLast ? sb : nxt + BM * 128;
+      const int ksn = ks < kLast ? ks + 1 : 0;
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -302,19 +316,21 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
             opb.issue(rb, nxt + BM * 128, q - PA, kn);
           }
         }
-        if (ks + 1 < kBK / 16) {
-          fa[nx][i] = opa.frag(sa, wave_m * WTM + i * 32, ks + 1, lane);
-          if (i < TN) fb[nx][i] = opb.frag(sb, wave_n * WTN + i * 32, ks + 1, lane);
-        }
+        fa[nx][i] = opa.frag(ra_, wave_m * WTM + i * 32, ksn, lane);
+        if (i < TN) fb[nx][i] = opb.frag(rb_, wave_n * WTN + i * 32, ksn, lane);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    wait_vmem();
-    __syncthreads();
   }
+  // The last prefetch (of a tile that is never computed) may still be in flight. Inline-asm reads
+  // land in their registers asynchronously, so they must be waited for while the registers are
+  // still theirs: the wait carries them as operands.
+  if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[0]);
   if constexpr (kAnyTail) {
     if (tail_here) {
-      // the last K-tile of a K that is not a multiple of 64, staged outside the pipeline
+      // the last K-tile of a K that is not a multiple of 64, staged outside the pipeline (after
+      // every wave's last fragment reads of the stage it overwrites)
+      __syncthreads();
       if constexpr (AOP::kNeedsTail)
         opa.tail(ra, smem, kfull, a.K, lane);
       else
@@ -383,30 +399,55 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
         }
     }
   } else {
-    uint16_t *C = (uint16_t *)a.C;
+    // The C tile goes through LDS (free after the main loop): each wave parks its WTM x WTN
+    // sub-tile there as paired 4-byte writes, then reads it back along rows and stores 16 bytes
+    // per lane, so one store instruction writes whole 256-byte row segments (two cache lines)
+    // instead of sixteen half lines.
+    constexpr int kRowB = WTN * 2;       // bytes per sub-tile row
+    constexpr int kChunks = kRowB / 16;  // 16-byte chunks per row
+    static_assert(kChunks == 16 || kChunks == 8, "sub-tile width");
+    static_assert(4 * WTM * kRowB <= 2 * kStage, "C tile fits the LDS stages");
+    // chunk swizzle: the four rows one paired write instruction touches land on disjoint banks
+    auto swz = [](int rr) { return kChunks == 16 ? 4 * ((rr & 1) | ((rr >> 1) & 2)) : 4 * ((rr >> 2) & 1); };
+    __syncthreads();  // every wave is done reading the last K-tile's fragments
+    char *ct = smem + wave * (WTM * kRowB);
     const uint16_t *bias = (const uint16_t *)a.bias;
-    const bool vec = (a.ldc & 1) == 0;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int col = nw + j * 32;
-      const int own = col + (odd ? 1 : 0);  // the column this lane's accumulators belong to
+      const int own = nw + j * 32 + (odd ? 1 : 0);  // the column this lane's accumulators belong to
       const float bv = (a.has_bias && own < a.N) ? from_bits<DT>(bias[own]) : 0.0f;
+      const int cc = col_l + j * 32;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int r = 0; r < 16; r += 2) {
           float lo, hi;
           pair(acc[i][j][r] + bv, acc[i][j][r + 1] + bv, lo, hi);
-          const int row = mw + i * 32 + 8 * (r >> 2) + (r & 3);
-          if (row < a.M) {
-            if (vec && col + 1 < a.N) {
-              *(uint32_t *)(C + (size_t)row * a.ldc + col) = pack2<DT>(lo, hi);
-            } else {
-              if (col < a.N) C[(size_t)row * a.ldc + col] = to_bits<DT>(lo);
-              if (col + 1 < a.N) C[(size_t)row * a.ldc + col + 1] = to_bits<DT>(hi);
-            }
+          const int rr = row_l + i * 32 + 8 * (r >> 2) + (r & 3);
+          *(uint32_t *)(ct + rr * kRowB + (((cc >> 3) ^ swz(rr)) << 4) + (cc & 7) * 2) = pack2<DT>(lo, hi);
+        }
+    }
+    uint16_t *C = (uint16_t *)a.C;
+    const bool v16 = (a.ldc & 7) == 0 && ((uintptr_t)a.C & 15) == 0;
+    const int gr0 = m0 + wave_m * WTM, gc0 = n0 + wave_n * WTN;
+    constexpr int kRowsPerInst = 64 / kChunks;
+#pragma unroll 4
+    for (int it = 0; it < WTM / kRowsPerInst; ++it) {
+      const int rr = it * kRowsPerInst + lane / kChunks, ch = lane % kChunks;
+      const u32x4 v = *(const u32x4 *)(ct + rr * kRowB + ((ch ^ swz(rr)) << 4));
+      const int grow = gr0 + rr, gcol = gc0 + 8 * ch;
+      if (grow < a.M) {
+        uint16_t *dst = C + (size_t)grow * a.ldc + gcol;
+        if (v16 && gcol + 8 <= a.N) {
+          *(u32x4 *)dst = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t w = v[e >> 1];
+            if (gcol + e < a.N) dst[e] = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
           }
         }
+      }
     }
   }
 }
