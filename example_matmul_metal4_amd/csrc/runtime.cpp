@@ -182,9 +182,12 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   if (d.ldc < d.N) return fail(MTK_ERR_INVALID, "ldc (%d) < N (%d)", d.ldc, d.N);
   if (d.split_k < 0) return fail(MTK_ERR_INVALID, "split_k must be >= 0");
   if (d.tile != 0 && d.tile != 128 && d.tile != 256) return fail(MTK_ERR_INVALID, "tile must be 0, 128 or 256");
-  const uint64_t a_bytes = ((uint64_t)(d.M - 1) * d.lda + d.K) * 2;
+  // Buffer ranges end on a whole dword: raw buffer loads range-check per dword, so a last element
+  // in the low half of a straddling dword would read as zero. The at most 2 extra bytes lie in the
+  // same aligned dword (same page) as the operand's last element; they are masked in the kernels.
+  const uint64_t a_bytes = (((uint64_t)(d.M - 1) * d.lda + d.K) * 2 + 3) & ~3ull;
   const uint64_t b_rows = d.trans_b ? d.N : d.K, b_cols = d.trans_b ? d.K : d.N;
-  const uint64_t b_bytes = ((b_rows - 1) * (uint64_t)d.ldb + b_cols) * 2;
+  const uint64_t b_bytes = (((b_rows - 1) * (uint64_t)d.ldb + b_cols) * 2 + 3) & ~3ull;
   if (a_bytes > kMaxOperandBytes || b_bytes > kMaxOperandBytes)
     return fail(MTK_ERR_UNSUPPORTED, "operands above 2 GiB are not supported by this build");
 

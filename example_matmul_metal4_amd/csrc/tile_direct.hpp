@@ -9,8 +9,10 @@
 // Staging: gfx950 direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds). One wave instruction
 // writes 1 KB of LDS, lane l to byte 16*l; each policy hands every lane the global address of the
 // 16 bytes that belong at that slot, so swizzles are applied on the global side. Out-of-range
-// offsets read as zero and are written to LDS as zero: rows past M/N, the K tail (whole chunks)
-// and convolution padding all cost nothing but an offset select.
+// offsets read as zero and are written to LDS as zero: rows past M/N, rows past K of a K-major
+// operand and convolution padding cost nothing but an offset select. A partial last K-tile of a
+// K-contiguous operand is loaded whole and its fragments are masked at K in registers; it runs in
+// the same pipeline as the full tiles.
 //
 // Fragments: [rows][64] tiles use ds_read_b128 with the chunk swizzle chunk ^ (row&7) ^ ((row>>3)&7);
 // the [64][cols] tile uses two ds_read_b64_tr_b16 per fragment: in each 16-lane group, lane s
@@ -38,7 +40,7 @@ namespace mtk {
 template <int ROWS>
 struct OpRows {
   static constexpr int kLoads = ROWS / 32;  // 1 KB blocks per wave per K-tile
-  static constexpr bool kNeedsTail = true;  // a K that is not a multiple of 8 needs element masks
+  static constexpr bool kNeedsTail = true;  // the last K-tile's fragments are masked at K
   static constexpr bool kAsmFrag = false;
   uint32_t off[kLoads];
   int blk0;
@@ -57,27 +59,21 @@ struct OpRows {
   __device__ __forceinline__ void issue(rsrc_t r, char *lds, int q, int kt) const {
     lds_direct16(r, lds + (blk0 + q) * 1024, off[q] + (uint32_t)kt * 128u);
   }
-  // Partial last K-tile: element-masked register loads into the same physical layout.
-  __device__ void tail(rsrc_t r, char *lds, int kt, int K, int lane) const {
-    const int cbase = (lane & 7) ^ (lane >> 3);
+  // The last K-tile of a K that is not a multiple of 64 is loaded whole (chunks past K hold the
+  // next row's elements, or zeros past the operand); its fragments are masked before use. A
+  // fragment holds the 8 elements k0 .. k0+7 of one row.
+  __device__ static __forceinline__ u32x4 mask(u32x4 v, int k0, int K) {
+    const int n = K - k0;  // valid elements in this chunk
+    u32x4 r;
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int k = kt * kBK + 8 * (cbase ^ ((blk0 + i) & 7));
-      const uint32_t o = off[i] + (uint32_t)kt * 128u;
-      u32x4 v;
-      if (k >= K) {
-        v = u32x4{};
-      } else if (k + 8 <= K) {
-        v = buf_load16(r, o);
-      } else {
-        uint32_t h[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) h[e] = buf_load2(r, k + e < K ? o + 2u * e : kOOB);
-        v = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-      }
-      *(u32x4 *)(lds + (blk0 + i) * 1024 + lane * 16) = v;
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t keep = 2 * d + 1 < n ? 0xffffffffu : (2 * d < n ? 0x0000ffffu : 0u);
+      r[d] = v[d] & keep;
     }
+    return r;
   }
+  // K offset of the fragment a lane reads for k-step ks of K-tile kt
+  __device__ static __forceinline__ int frag_k0(int kt, int ks, int lane) { return kt * kBK + 16 * ks + 8 * (lane >> 5); }
   __device__ __forceinline__ u32x4 frag(const char *lds, int rowblk, int ks, int lane) const {
     return *(const u32x4 *)(lds + lds_off(rowblk + (lane & 31), 2 * ks + (lane >> 5)));
   }
@@ -262,7 +258,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
 
-  if (kt0 < kfull) issue_all(smem, kt0);
+  if (kt0 < kt1) issue_all(smem, kt0);
   wait_vmem();
   __syncthreads();
 
@@ -278,9 +274,10 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   for (int kt = kt0; kt < kfull; ++kt) {
     const int cur = (kt - kt0) & 1;
     char *nxt = smem + (cur ^ 1) * kStage;
-    // Branch-free prefetch: on the last full tile this reloads the current tile into the idle
-    // stage (L2 hits, never read) instead of reaching into another split's K range.
-    const int kn = min(kt + 1, kfull - 1);
+    // The next tile is the partial last K-tile when there is one. Without one, the last iteration
+    // reloads the current tile into the idle stage (L2 hits, never computed) instead of reaching
+    // into another split's K range: branch-free.
+    const int kn = min(kt + 1, kt1 - 1);
     const char *sa = smem + cur * kStage;
     const char *sb = sa + BM * 128;
     typename std::conditional<std::is_same<AOP, OpConv<BM>>::value, typename OpConv<BM>::Tap, int>::type tp{};
@@ -328,31 +325,32 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[0]);
   if constexpr (kAnyTail) {
     if (tail_here) {
-      // the last K-tile of a K that is not a multiple of 64, staged outside the pipeline (after
-      // every wave's last fragment reads of the stage it overwrites)
-      __syncthreads();
-      if constexpr (AOP::kNeedsTail)
-        opa.tail(ra, smem, kfull, a.K, lane);
-      else
-        for (int q = 0; q < PA; ++q) opa.issue(ra, smem, q, kfull);
-      if constexpr (BOP::kNeedsTail)
-        opb.tail(rb, smem + BM * 128, kfull, a.K, lane);
-      else
-        for (int q = 0; q < PB; ++q) opb.issue(rb, smem + BM * 128, q, kfull);
-      wait_vmem();
-      __syncthreads();
+      // The partial last K-tile, already in LDS (loaded as the last loop iteration's next tile,
+      // or by the prologue when it is the only tile): same k-steps, fragments masked at K.
+      const char *sa = smem + ((kfull - kt0) & 1) * kStage;
+      const char *sb = sa + BM * 128;
 #pragma unroll
       for (int ks = 0; ks < kBK / 16; ++ks) {
-        u32x4 fa1[TM], fb1[TN];
+        const int c = ks & 1, nx = c ^ 1;
+        if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[c]);
+        if constexpr (AOP::kNeedsTail) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) fa1[i] = opa.frag(smem, wave_m * WTM + i * 32, ks, lane);
+          for (int i = 0; i < TM; ++i) fa[c][i] = AOP::mask(fa[c][i], AOP::frag_k0(kfull, ks, lane), a.K);
+        }
+        if constexpr (BOP::kNeedsTail) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) fb1[j] = opb.frag(smem + BM * 128, wave_n * WTN + j * 32, ks, lane);
-        if constexpr (BOP::kAsmFrag) lgkm_wait0(fb1);
+          for (int j = 0; j < TN; ++j) fb[c][j] = BOP::mask(fb[c][j], BOP::frag_k0(kfull, ks, lane), a.K);
+        }
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) {
 #pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa1[i], fb1[j], acc[i][j]);
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa[c][i], fb[c][j], acc[i][j]);
+          if (ks + 1 < kBK / 16) {
+            fa[nx][i] = opa.frag(sa, wave_m * WTM + i * 32, ks + 1, lane);
+            if (i < TN) fb[nx][i] = opb.frag(sb, wave_n * WTN + i * 32, ks + 1, lane);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
   }

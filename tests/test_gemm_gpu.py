@@ -160,6 +160,37 @@ def test_strided_operands(dev):
         b.free()
 
 
+@pytest.mark.parametrize("M,N,K,lda,ldb,split_k", [
+    (100, 96, 131, 132, 134, 1),   # odd K, even leading dimensions: last element ends mid-dword
+    (70, 66, 131, 132, 132, 3),
+    (64, 80, 40, 40, 40, 1),       # K below one 64-deep tile: the partial tile is the only tile
+    (96, 64, 4100, 4100, 4100, 65),  # one K-tile per split: the last split holds only the partial tile
+    (256, 256, 4101, 4102, 4104, 4),
+])
+def test_partial_last_k_tile(dev, M, N, K, lda, ldb, split_k):
+    A = oracle.normal(50, (M, lda), 0, 1)
+    B = oracle.normal(51, (N, ldb), 0, 1)
+    bias = oracle.uniform(52, (N,), -0.5, 0.5)
+    print(f"[gemm] partial K tile M={M} N={N} K={K} lda={lda} ldb={ldb} split_k={split_k}", flush=True)
+    plan = mtk.GemmPlan(dev, M, N, K, has_bias=True, lda=lda, ldb=ldb, split_k=split_k)
+    assert "direct-to-LDS" in plan.describe()
+    dA, dB, db = dev.upload(A), dev.upload(B), dev.upload(bias)
+    dC = dev.empty(M * N * 2)
+    ws = dev.empty(plan.workspace_bytes) if plan.workspace_bytes else None
+    plan.run(dA, dB, db, dC, ws)
+    dev.sync()
+    C = dev.download(dC, (M, N), np.float16)
+    a, b = np.ascontiguousarray(A[:, :K]), np.ascontiguousarray(B[:, :K])
+    exp = oracle.gemm(a, b, bias)
+    absdot = np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64)).T + np.abs(bias.astype(np.float64))
+    res = oracle.compare(C.astype(np.float64), exp, bound=oracle.dot_bound(exp, absdot, K))
+    print(f"   {res}", flush=True)
+    assert res["ok"], res
+    for x in (dA, dB, db, dC, ws):
+        if x is not None:
+            x.free()
+
+
 def test_run_errors(dev):
     plan = mtk.GemmPlan(dev, 64, 64, 512, has_bias=True, split_k=2)
     assert plan.workspace_bytes == 2 * 64 * 64 * 4
