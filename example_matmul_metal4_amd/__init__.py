@@ -67,7 +67,7 @@ class DeviceInfo(ctypes.Structure):
 
 class GemmDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("M", "N", "K", "lda", "ldb", "ldc", "trans_b", "dtype", "has_bias",
-                                            "split_k", "tile")]
+                                            "split_k", "tile", "trans_a")]
 
 
 class GemmArgs(ctypes.Structure):
@@ -308,15 +308,17 @@ def _ptr(x):
 
 
 class GemmPlan(_Plan):
-    """C[M][N] = bias + A[M][K] . op(B); B is [N][K] when trans_b (the reference default) else [K][N]."""
+    """C[M][N] = bias + op(A) . op(B); A is [M][K] (default) or [K][M] when trans_a (the reference's
+    transpose.left); B is [N][K] when trans_b (the reference default) else [K][N]."""
 
     _args_type = GemmArgs
     _run_fn = "mtk_gemm_run"
 
     def __init__(self, device: Device | None, M, N, K, *, trans_b=True, dtype="f16", has_bias=False, split_k=1,
-                 tile=0, lda=0, ldb=0, ldc=0):
+                 tile=0, lda=0, ldb=0, ldc=0, trans_a=False):
         self.desc = GemmDesc(M=M, N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, trans_b=1 if trans_b else 0,
-                             dtype=_DT[dtype], has_bias=1 if has_bias else 0, split_k=split_k, tile=tile)
+                             dtype=_DT[dtype], has_bias=1 if has_bias else 0, split_k=split_k, tile=tile,
+                             trans_a=1 if trans_a else 0)
         h = ctypes.c_void_p()
         _check(lib().mtk_gemm_plan(device.handle if device else None, ctypes.byref(self.desc), ctypes.byref(h)))
         super().__init__(h)
@@ -391,12 +393,15 @@ class ConvPlan(_Plan):
 
 # ------------------------------------------------------------------ harness-level calls
 
-def gemm(dev: Device, A, B, bias=None, *, trans_b=True, dtype="f16", split_k=1, tile=0) -> np.ndarray:
-    """matmul.run equivalent: upload, plan, run, read back C (same 16-bit dtype as the inputs)."""
+def gemm(dev: Device, A, B, bias=None, *, trans_b=True, dtype="f16", split_k=1, tile=0,
+         trans_a=False) -> np.ndarray:
+    """matmul.run equivalent: upload, plan, run, read back C (same 16-bit dtype as the inputs).
+    A is [M][K], or [K][M] with trans_a; B is [N][K] with trans_b, else [K][N]."""
     A, B = _bits(A), _bits(B)
-    M, K = A.shape
+    K, M = A.shape if trans_a else A.shape[::-1]
     N = B.shape[0] if trans_b else B.shape[1]
-    plan = GemmPlan(dev, M, N, K, trans_b=trans_b, dtype=dtype, has_bias=bias is not None, split_k=split_k, tile=tile)
+    plan = GemmPlan(dev, M, N, K, trans_b=trans_b, dtype=dtype, has_bias=bias is not None, split_k=split_k, tile=tile,
+                    trans_a=trans_a)
     dA, dB = dev.upload(A), dev.upload(B)
     dbias = dev.upload(_bits(bias)) if bias is not None else None
     dC = dev.empty(M * N * 2)

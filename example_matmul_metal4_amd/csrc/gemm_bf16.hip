@@ -1,6 +1,7 @@
 // bf16 GEMM instantiations. Kernel names are what the runtime's kernel-select looks up.
 //   *_nt_*_d   B [N][K] (the reference's default layout), direct-to-LDS pipeline
 //   *_nn_*_d   B [K][N] (config 1 "C = A.B row-major"), direct-to-LDS + transposed LDS reads
+//   *_tt_*_d, *_tn_*_d   A [K][M] (the reference's transpose.left) with B [N][K] / [K][N]
 //   *_v1       2-byte register-staged fallback for odd leading dimensions
 // plus the split-K second pass.
 #include "tile_direct.hpp"
@@ -21,6 +22,10 @@ DIRECT_KERNEL(mtk_gemm_bf16_nt_256x256_d, DT_BF16, 256, 256, OpRows<256>, OpRows
 DIRECT_KERNEL(mtk_gemm_bf16_nt_128x128_d, DT_BF16, 128, 128, OpRows<128>, OpRows<128>)
 DIRECT_KERNEL(mtk_gemm_bf16_nn_256x256_d, DT_BF16, 256, 256, OpRows<256>, OpColsT<256>)
 DIRECT_KERNEL(mtk_gemm_bf16_nn_128x128_d, DT_BF16, 128, 128, OpRows<128>, OpColsT<128>)
+DIRECT_KERNEL(mtk_gemm_bf16_tt_256x256_d, DT_BF16, 256, 256, OpColsT<256>, OpRows<256>)
+DIRECT_KERNEL(mtk_gemm_bf16_tt_128x128_d, DT_BF16, 128, 128, OpColsT<128>, OpRows<128>)
+DIRECT_KERNEL(mtk_gemm_bf16_tn_256x256_d, DT_BF16, 256, 256, OpColsT<256>, OpColsT<256>)
+DIRECT_KERNEL(mtk_gemm_bf16_tn_128x128_d, DT_BF16, 128, 128, OpColsT<128>, OpColsT<128>)
 
 TILE_KERNEL(mtk_gemm_bf16_nt_256x256_v1, DT_BF16, 256, 256, 2, 2, A_MK, B_NK, 1, 1)
 TILE_KERNEL(mtk_gemm_bf16_nt_128x128_v1, DT_BF16, 128, 128, 2, 2, A_MK, B_NK, 1, 1)

@@ -174,10 +174,13 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   mtk_gemm_desc d = *d_in;
   if (d.M <= 0 || d.N <= 0 || d.K <= 0) return fail(MTK_ERR_INVALID, "M, N, K must be positive (got %d, %d, %d)", d.M, d.N, d.K);
   if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "GEMM dtype must be MTK_F16 or MTK_BF16");
-  if (d.lda == 0) d.lda = d.K;
+  d.trans_a = d.trans_a ? 1 : 0;
+  if (d.lda == 0) d.lda = d.trans_a ? d.M : d.K;
   if (d.ldb == 0) d.ldb = d.trans_b ? d.K : d.N;
   if (d.ldc == 0) d.ldc = d.N;
-  if (d.lda < d.K) return fail(MTK_ERR_INVALID, "lda (%d) < K (%d)", d.lda, d.K);
+  if (d.lda < (d.trans_a ? d.M : d.K)) return fail(MTK_ERR_INVALID, "lda (%d) too small", d.lda);
+  if (d.trans_a && d.lda % 2 != 0)
+    return fail(MTK_ERR_UNSUPPORTED, "trans_a needs an even lda (4-byte aligned rows of A [K][lda])");
   if (d.ldb < (d.trans_b ? d.K : d.N)) return fail(MTK_ERR_INVALID, "ldb (%d) too small", d.ldb);
   if (d.ldc < d.N) return fail(MTK_ERR_INVALID, "ldc (%d) < N (%d)", d.ldc, d.N);
   if (d.split_k < 0) return fail(MTK_ERR_INVALID, "split_k must be >= 0");
@@ -185,7 +188,8 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   // Buffer ranges end on a whole dword: raw buffer loads range-check per dword, so a last element
   // in the low half of a straddling dword would read as zero. The at most 2 extra bytes lie in the
   // same aligned dword (same page) as the operand's last element; they are masked in the kernels.
-  const uint64_t a_bytes = (((uint64_t)(d.M - 1) * d.lda + d.K) * 2 + 3) & ~3ull;
+  const uint64_t a_rows = d.trans_a ? d.K : d.M, a_cols = d.trans_a ? d.M : d.K;
+  const uint64_t a_bytes = (((a_rows - 1) * (uint64_t)d.lda + a_cols) * 2 + 3) & ~3ull;
   const uint64_t b_rows = d.trans_b ? d.N : d.K, b_cols = d.trans_b ? d.K : d.N;
   const uint64_t b_bytes = (((b_rows - 1) * (uint64_t)d.ldb + b_cols) * 2 + 3) & ~3ull;
   if (a_bytes > kMaxOperandBytes || b_bytes > kMaxOperandBytes)
@@ -203,7 +207,7 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   // Decode-shaped problems (M <= 16, B [N][K]) go to the HBM-streaming skinny kernel; its
   // split-K partitions are wavefronts of one workgroup, reduced on chip with the bias fused. The
   // grid is persistent: one workgroup per CU walking the 16-column groups.
-  if (d.M <= 16 && d.trans_b && d.tile == 0 && d.K % 8 == 0 && d.lda % 8 == 0 && d.ldb % 8 == 0) {
+  if (d.M <= 16 && !d.trans_a && d.trans_b && d.tile == 0 && d.K % 8 == 0 && d.lda % 8 == 0 && d.ldb % 8 == 0) {
     int split = d.split_k == 0 ? (d.K >= 1024 ? 8 : std::max(1, d.K / 128)) : d.split_k;
     split = std::max(1, std::min(split, 8));
     int kps = ((d.K + split - 1) / split + 31) / 32 * 32;
@@ -270,7 +274,9 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
 
   Launch g;
   char name[96];
-  snprintf(name, sizeof name, "mtk_gemm_%s_%s_%dx%d_%s", dt, d.trans_b ? "nt" : "nn", tile, tile, direct ? "d" : "v1");
+  // operand letters: A [M][K] 'n' / [K][M] 't', B [N][K] 't' / [K][N] 'n'
+  snprintf(name, sizeof name, "mtk_gemm_%s_%c%c_%dx%d_%s", dt, d.trans_a ? 't' : 'n', d.trans_b ? 't' : 'n', tile, tile,
+           direct ? "d" : "v1");
   g.name = name;
   g.grid = (unsigned)(tiles * split);
   mtk_tile_args a{};
@@ -308,8 +314,8 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
     p->launches.push_back(r);
   }
   char desc[256];
-  snprintf(desc, sizeof desc, "gemm %s %s M=%d N=%d K=%d tile=%dx%d split_k=%d k_tiles/split=%d %s grid=%u%s",
-           dt, d.trans_b ? "B[N][K]" : "B[K][N]", d.M, d.N, d.K, tile, tile, split, kps,
+  snprintf(desc, sizeof desc, "gemm %s %s %s M=%d N=%d K=%d tile=%dx%d split_k=%d k_tiles/split=%d %s grid=%u%s",
+           dt, d.trans_a ? "A[K][M]" : "A[M][K]", d.trans_b ? "B[N][K]" : "B[K][N]", d.M, d.N, d.K, tile, tile, split, kps,
            direct ? "direct-to-LDS" : "2-byte loads", g.grid,
            split > 1 ? " + splitk_reduce" : "");
   p->description = desc;

@@ -3,6 +3,7 @@
 // C[M][N] (+ bias) = A . B with A and B given by policies:
 //   A: OpRows  (A [M][lda] row-major, the reference GEMM)            -> LDS [BM][64]
 //      OpConv  (implicit-GEMM gather of an NDHWC activation, C%64==0) -> LDS [BM][64]
+//      OpColsT (A [K][lda]: the reference's transpose.left)           -> LDS [64][BM]
 //   B: OpRows  (B [N][ldb], the reference's default transpose.right)  -> LDS [BN][64]
 //      OpColsT (B [K][ldb]: GEMM B [K][N], DHWIO conv weights [K][O])  -> LDS [64][BN]
 //
@@ -227,7 +228,6 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   const int kt0 = split * a.k_tiles_per_split;
   const int kt1 = min(kt0 + a.k_tiles_per_split, a.k_tiles);
   constexpr bool kAnyTail = AOP::kNeedsTail || BOP::kNeedsTail;
-  static_assert(!AOP::kAsmFrag, "A fragments are read by compiler-visible loads");
   const bool tail_here = kAnyTail && (a.K % kBK) != 0 && kt1 == a.k_tiles && kt0 < kt1;
   const int kfull = tail_here ? kt1 - 1 : kt1;
 
@@ -293,7 +293,9 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
         wait_vmem();
         __syncthreads();
       }
-      if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[c]);  // this k-step's B fragments (read a step earlier)
+      // this k-step's fragments read by inline asm (one k-step earlier)
+      if constexpr (AOP::kAsmFrag) lgkm_wait0(fa[c]);
+      if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[c]);
       const char *ra_ = ks < kLast ? sa : nxt;
       const char *rb_ = ks < kLast ? sb : nxt + BM * 128;
       const int ksn = ks < kLast ? ks + 1 : 0;
@@ -322,6 +324,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   // The last prefetch (of a tile that is never computed) may still be in flight. Inline-asm reads
   // land in their registers asynchronously, so they must be waited for while the registers are
   // still theirs: the wait carries them as operands.
+  if constexpr (AOP::kAsmFrag) lgkm_wait0(fa[0]);
   if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[0]);
   if constexpr (kAnyTail) {
     if (tail_here) {
@@ -332,6 +335,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
 #pragma unroll
       for (int ks = 0; ks < kBK / 16; ++ks) {
         const int c = ks & 1, nx = c ^ 1;
+        if constexpr (AOP::kAsmFrag) lgkm_wait0(fa[c]);
         if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[c]);
         if constexpr (AOP::kNeedsTail) {
 #pragma unroll

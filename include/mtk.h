@@ -96,8 +96,10 @@ int mtk_set_stream(mtk_ctx *ctx, void *hip_stream);
 
 /* Replaces GEMMDimensions / BuildOptions{splitK, swapMN, ...} and the M,N,K function
  * constants (Sources/matmul/matmul.swift:5-16, 232-234, 372-378).
- * C[m][n] = bias[n] + sum_k A[m][k] * op(B)[k][n]
- *   A: [M][lda] row-major (lda >= K)
+ * C[m][n] = bias[n] + sum_k op(A)[m][k] * op(B)[k][n]
+ *   A: trans_a == 0 -> [M][lda] row-major (lda >= K), the reference default;
+ *      trans_a != 0 -> [K][lda] (lda >= M, even), the reference's transpose.left
+ *      (createSource(transpose: (true, _)), matmul.swift:72-90)
  *   B: trans_b != 0 -> [N][ldb] (the reference default, createSource(transpose: (false, true)),
  *      matmul.swift:366); trans_b == 0 -> [K][ldb]
  *   C: [M][ldc] row-major; bias: [N] (same dtype) or NULL.
@@ -107,12 +109,13 @@ int mtk_set_stream(mtk_ctx *ctx, void *hip_stream);
  * tile: 0 = let the plan choose; else 128 or 256 (square MFMA workgroup tile). */
 typedef struct {
   int M, N, K;
-  int lda, ldb, ldc; /* 0 = packed (K, K or N, N) */
+  int lda, ldb, ldc; /* 0 = packed (K or M, K or N, N) */
   int trans_b;
   int dtype;          /* MTK_F16 or MTK_BF16 */
   int has_bias;
   int split_k;
   int tile;
+  int trans_a; /* appended: earlier fields keep their offsets */
 } mtk_gemm_desc;
 
 /* Kernel-select. Replaces createSource(...) + makeLibrary + makeFunction(name:constantValues:) +

@@ -40,6 +40,7 @@ def test_code_objects_hold_every_selectable_kernel():
                      for f in os.listdir(mtk.LIB_DIR) if f.endswith(".hsaco"))
     names = [f"mtk_gemm_{dt}_{lay}_{t}x{t}_{v}" for dt in ("f16", "bf16") for lay in ("nt", "nn") for t in (128, 256)
              for v in ("d", "v1")]
+    names += [f"mtk_gemm_{dt}_{lay}_{t}x{t}_d" for dt in ("f16", "bf16") for lay in ("tt", "tn") for t in (128, 256)]
     names += ["mtk_splitk_reduce_f16", "mtk_splitk_reduce_bf16", "mtk_fill_u16", "mtk_skinny_f16", "mtk_skinny_bf16",
               "mtk_skinny_f16_long", "mtk_skinny_bf16_long"]
     names += [f"mtk_attn_fwd_{dt}{c}" for dt in ("f16", "bf16") for c in ("", "_causal")]
@@ -92,6 +93,11 @@ def test_gemm_kernel_select_dry():
     p = mtk.GemmPlan(None, 8, 14336, 8192, split_k=4)
     assert "mtk_skinny_f16_long" in p.describe() and "grid=256 " in p.describe()
     assert "grid=3 " in mtk.GemmPlan(None, 8, 40, 256, split_k=2).describe()
+    # transpose.left: A [K][M] through the transposed-read policy; never the skinny path
+    p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4, trans_a=True)
+    assert "mtk_gemm_f16_tt_256x256_d" in p.describe() and "A[K][M]" in p.describe()
+    assert "mtk_gemm_bf16_tn_128x128_d" in mtk.GemmPlan(None, 16, 64, 64, dtype="bf16", trans_a=True,
+                                                          trans_b=False).describe()
     # split-K never produces an empty split
     p = mtk.GemmPlan(None, 64, 64, 100, split_k=8)
     assert "split_k=2 k_tiles/split=1" in p.describe()
@@ -105,6 +111,8 @@ def test_gemm_kernel_select_dry():
     (dict(M=4, N=4, K=8, split_k=-2), mtk.MTK_ERR_INVALID),
     (dict(M=4, N=4, K=8, tile=64), mtk.MTK_ERR_INVALID),
     (dict(M=70000, N=4, K=20000), mtk.MTK_ERR_UNSUPPORTED),
+    (dict(M=8, N=4, K=8, trans_a=True, lda=6), mtk.MTK_ERR_INVALID),        # lda < M
+    (dict(M=7, N=4, K=8, trans_a=True), mtk.MTK_ERR_UNSUPPORTED),           # odd lda for A [K][M]
 ])
 def test_gemm_descriptor_validation(kw, status):
     M, N, K = kw.pop("M"), kw.pop("N"), kw.pop("K")

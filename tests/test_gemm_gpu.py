@@ -191,6 +191,37 @@ def test_partial_last_k_tile(dev, M, N, K, lda, ldb, split_k):
             x.free()
 
 
+@pytest.mark.parametrize("M,N,K,trans_b,dtype,split_k,tile", [
+    (256, 256, 256, True, "f16", 1, 0),
+    (300, 200, 1000, True, "f16", 1, 0),     # ragged tiles, K tail on B only
+    (300, 200, 1000, False, "f16", 3, 0),    # A [K][M] and B [K][N]: both operands K-major
+    (512, 512, 4100, True, "bf16", 4, 256),
+    (130, 514, 700, False, "bf16", 1, 128),
+    (64, 96, 72, True, "f16", 2, 0),
+])
+def test_transpose_left(dev, M, N, K, trans_b, dtype, split_k, tile):
+    # The reference's transpose.left: A stored [K][M] (matmul.swift:72-90). The oracle takes A as
+    # [M][K], so it is given the host transpose of the same data.
+    At = oracle.normal(60, (K, M), 0, 1 / np.sqrt(K), dtype)
+    B = oracle.normal(61, (N, K) if trans_b else (K, N), 0, 1 / np.sqrt(K), dtype)
+    bias = oracle.uniform(62, (N,), -0.5, 0.5, dtype)
+    print(f"[gemm] transpose.left M={M} N={N} K={K} trans_b={trans_b} {dtype} split_k={split_k} tile={tile}",
+          flush=True)
+    got = mtk.gemm(dev, At, B, bias, trans_a=True, trans_b=trans_b, dtype=dtype, split_k=split_k, tile=tile)
+    A = np.ascontiguousarray(At.T)
+    exp = oracle.gemm(A, B, bias, trans_b=trans_b, dtype=dtype)
+    a, b = _f32(A, dtype), _f32(B, dtype)
+    absdot = np.abs(a) @ (np.abs(b).T if trans_b else np.abs(b)) + np.abs(_f32(bias, dtype))
+    rel_tol = 1e-3 + (oracle.rel_frobenius(oracle.to_f32(oracle.from_f32(exp, dtype), dtype), exp)
+                      if dtype == "bf16" else 0.0)
+    res = oracle.compare(_f32(got, dtype), exp, bound=oracle.dot_bound(exp, absdot, K, dtype), rel_tol=rel_tol)
+    print(f"   {res}", flush=True)
+    assert res["ok"], res
+    # same numbers as the default layout of the same data (different summation split: tolerance)
+    ref = mtk.gemm(dev, A, B, bias, trans_b=trans_b, dtype=dtype, split_k=split_k, tile=tile)
+    assert oracle.compare(_f32(got, dtype), _f32(ref, dtype), rel_tol=rel_tol)["ok"]
+
+
 def test_run_errors(dev):
     plan = mtk.GemmPlan(dev, 64, 64, 512, has_bias=True, split_k=2)
     assert plan.workspace_bytes == 2 * 64 * 64 * 4
