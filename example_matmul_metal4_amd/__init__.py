@@ -138,6 +138,9 @@ SIGNATURES = {
     "mtk_plan_work": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "mtk_plan_destroy": (ctypes.c_int, [_VP]),
     "mtk_profile": (ctypes.c_int, [_VP, _VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(Timing)]),
+    "mtk_graph_create": (ctypes.c_int, [_VP, _VP, ctypes.c_int, ctypes.c_int, _PP]),
+    "mtk_graph_launch": (ctypes.c_int, [_VP]),
+    "mtk_graph_destroy": (ctypes.c_int, [_VP]),
     "mtk_validate_f16": (ctypes.c_int, [_VP, ctypes.c_int, _VP, ctypes.c_size_t, ctypes.c_double,
                                         ctypes.POINTER(Validation)]),
 }
@@ -224,6 +227,12 @@ class Device:
         _check(lib().mtk_upload(self.handle, ctypes.c_void_p(b.ptr), host.ctypes.data_as(ctypes.c_void_p), host.nbytes))
         return b
 
+    def upload_into(self, buf: DeviceBuffer, host: np.ndarray):
+        """Copy host data into an existing buffer (ordered on the context's stream, then waits)."""
+        host = np.ascontiguousarray(host)
+        assert host.nbytes <= buf.nbytes
+        _check(lib().mtk_upload(self.handle, ctypes.c_void_p(buf.ptr), host.ctypes.data_as(ctypes.c_void_p), host.nbytes))
+
     def download(self, buf: DeviceBuffer, shape, dtype) -> np.ndarray:
         out = np.empty(shape, dtype)
         assert out.nbytes <= buf.nbytes
@@ -299,6 +308,37 @@ class _Plan:
         _check(lib().mtk_profile(self.handle, ctypes.cast(arr, ctypes.c_void_p), len(arg_sets), warmup, iters,
                                  ctypes.byref(t)))
         return t.as_dict()
+
+    def graph(self, arg_sets, steps: int) -> "Graph":
+        """`steps` runs (argument set i % len(arg_sets) for run i) recorded as one HIP graph: the
+        duplicatedCount dispatches of one command buffer. The argument buffers must outlive it."""
+        arr = (self._args_type * len(arg_sets))(*arg_sets)
+        h = ctypes.c_void_p()
+        _check(lib().mtk_graph_create(self.handle, ctypes.cast(arr, ctypes.c_void_p), len(arg_sets), steps,
+                                      ctypes.byref(h)))
+        return Graph(h)
+
+
+class Graph:
+    """An instantiated HIP graph of repeated plan runs (mtk_graph_*)."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    def launch(self):
+        """Enqueue every recorded run on the context's stream (does not wait)."""
+        _check(lib().mtk_graph_launch(self.handle))
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().mtk_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def _ptr(x):

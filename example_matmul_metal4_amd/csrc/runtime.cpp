@@ -70,8 +70,9 @@ struct mtk_ctx {
         *f = fn;
         return MTK_OK;
       }
+      // a miss in one module is expected; leave no sticky error for the caller's next HIP call
+      (void)hipGetLastError();
     }
-    (void)hipGetLastError();
     return fail(MTK_ERR_MODULE, "kernel %s not found in the loaded code objects", name.c_str());
   }
 };
@@ -849,6 +850,66 @@ int mtk_plan_work(const mtk_plan *plan, double *flops, double *bytes) {
 
 int mtk_plan_destroy(mtk_plan *plan) {
   delete plan;
+  return MTK_OK;
+}
+
+struct mtk_graph {
+  mtk_ctx *ctx = nullptr;
+  hipStream_t stream = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+int mtk_graph_create(const mtk_plan *p, const void *arg_sets, int nsets, int steps, mtk_graph **out) {
+  if (!p || !arg_sets || nsets <= 0 || steps <= 0 || !out) return fail(MTK_ERR_INVALID, "invalid graph arguments");
+  if (!p->ctx) return fail(MTK_ERR_INVALID, "plan was created without a context (dry plan)");
+  if (steps > 100000) return fail(MTK_ERR_INVALID, "steps above 100000");
+  *out = nullptr;
+  const size_t stride = argset_size(p);
+  std::vector<std::vector<Launch>> bound((size_t)nsets);
+  for (int i = 0; i < nsets; ++i) {
+    int s = bind_args(p, (const char *)arg_sets + stride * i, bound[(size_t)i]);
+    if (s != MTK_OK) return s;
+  }
+  HIP_TRY(hipSetDevice(p->ctx->device));
+  hipStream_t st = p->ctx->stream;
+  HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  int status = MTK_OK;
+  for (int i = 0; i < steps && status == MTK_OK; ++i) status = launch_all(p, bound[(size_t)(i % nsets)], nullptr);
+  hipGraph_t graph = nullptr;
+  const hipError_t ec = hipStreamEndCapture(st, &graph);
+  if (status != MTK_OK || ec != hipSuccess) {
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipGetLastError();
+    return status != MTK_OK ? status : fail(MTK_ERR_HIP, "stream capture failed: %s", hipGetErrorString(ec));
+  }
+  hipGraphExec_t exec = nullptr;
+  const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (ei != hipSuccess) {
+    (void)hipGraphDestroy(graph);
+    return fail(MTK_ERR_HIP, "graph instantiation failed: %s", hipGetErrorString(ei));
+  }
+  mtk_graph *g = new mtk_graph();
+  g->ctx = p->ctx;
+  g->stream = st;
+  g->graph = graph;
+  g->exec = exec;
+  *out = g;
+  return MTK_OK;
+}
+
+int mtk_graph_launch(mtk_graph *g) {
+  if (!g) return fail(MTK_ERR_INVALID, "null graph");
+  HIP_TRY(hipSetDevice(g->ctx->device));
+  HIP_TRY(hipGraphLaunch(g->exec, g->stream));
+  return MTK_OK;
+}
+
+int mtk_graph_destroy(mtk_graph *g) {
+  if (!g) return MTK_OK;
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  delete g;
   return MTK_OK;
 }
 

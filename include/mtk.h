@@ -220,6 +220,18 @@ typedef struct {
 
 int mtk_profile(const mtk_plan *plan, const void *arg_sets, int nsets, int warmup, int iters, mtk_timing *out);
 
+/* Repeated runs as one submission: replaces encoding `duplicatedCount` dispatches into one
+ * MTLCommandBuffer and committing it once (matmul.swift:447-449, 470-472; attention.swift:498;
+ * ConvolutionShared.swift:943-945). mtk_graph_create records `steps` runs of the plan (run i uses
+ * argument set i % nsets, each an mtk_*_args struct as for mtk_profile) into a HIP graph on the
+ * context's current stream and instantiates it; mtk_graph_launch enqueues all of them at once on
+ * that stream (does not wait). Arguments are bound at creation: the buffers must stay valid while
+ * the graph exists. The plan's kernels only (no memset nodes). */
+typedef struct mtk_graph mtk_graph;
+int mtk_graph_create(const mtk_plan *plan, const void *arg_sets, int nsets, int steps, mtk_graph **out);
+int mtk_graph_launch(mtk_graph *graph);
+int mtk_graph_destroy(mtk_graph *graph);
+
 /* ------------------------------------------------------------------ validate helpers */
 
 /* Compare a device result (16-bit dtype, n elements, on the host) against an fp32 expected
