@@ -45,7 +45,7 @@ typedef struct {
   int32_t M, N, ldc;
   int32_t split_k;
   int32_t has_bias;
-  int32_t vec8; /* 1: N, ldc multiple of 8 and C, bias 16-byte aligned -> 8-wide path */
+  int32_t vec4; /* 1: N, ldc multiple of 4 and C, bias 8-byte aligned -> 4-wide path */
 } mtk_reduce_args;
 
 /* 16-bit fill (zeroing workspaces inside a plan; graph-capturable, unlike hipMemsetAsync). */

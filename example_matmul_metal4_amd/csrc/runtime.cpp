@@ -308,8 +308,8 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
     ra.ldc = d.ldc;
     ra.split_k = split;
     ra.has_bias = a.has_bias;
-    ra.vec8 = (d.N % 8 == 0 && d.ldc % 8 == 0) ? 1 : 0;
-    const long long work = ra.vec8 ? (long long)d.M * d.N / 8 : (long long)d.M * d.N;
+    ra.vec4 = (d.N % 4 == 0 && d.ldc % 4 == 0) ? 1 : 0;
+    const long long work = ra.vec4 ? (long long)d.M * d.N / 4 : (long long)d.M * d.N;
     r.grid = (unsigned)std::min<long long>((work + 255) / 256, 65535);
     set_args(r, ra);
     p->launches.push_back(r);
@@ -563,7 +563,7 @@ int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
         r.partial = (const float *)g->workspace;
         r.bias = g->bias;
         r.C = g->C;
-        r.vec8 = r.vec8 && aligned(g->C, 16) && (!g->bias || aligned(g->bias, 16));
+        r.vec4 = r.vec4 && aligned(g->C, 8) && (!g->bias || aligned(g->bias, 8));
       }
     }
   } else if (p->kind == PLAN_CONV) {
