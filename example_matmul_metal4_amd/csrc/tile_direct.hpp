@@ -207,6 +207,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   // every load of the next K-tile is issued before the last k-step, where the barrier waits for it
   constexpr int kLoadGroups = MTK_LOAD_GROUPS < kGroups - TM ? MTK_LOAD_GROUPS : kGroups - TM;
   constexpr int kPerGroup = (PA + PB + kLoadGroups - 1) / kLoadGroups;
+  constexpr int kReadsPerGroup = (TM + TN + TM - 1) / TM;  // next k-step's fragment reads per MFMA group
 
   __shared__ __attribute__((aligned(1024))) char smem[2 * kStage];
 
@@ -315,8 +316,16 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
             opb.issue(rb, nxt + BM * 128, q - PA, kn);
           }
         }
-        fa[nx][i] = opa.frag(ra_, wave_m * WTM + i * 32, ksn, lane);
-        if (i < TN) fb[nx][i] = opb.frag(rb_, wave_n * WTN + i * 32, ksn, lane);
+        // The next k-step's first MFMA group needs every B fragment and only A fragment 0, later
+        // groups one more A fragment each: read the B fragments in the first groups, then A.
+#pragma unroll
+        for (int u = 0; u < kReadsPerGroup; ++u) {
+          const int slot = i * kReadsPerGroup + u;
+          if (slot < TN)
+            fb[nx][slot] = opb.frag(rb_, wave_n * WTN + slot * 32, ksn, lane);
+          else if (slot < TN + TM)
+            fa[nx][slot - TN] = opa.frag(ra_, wave_m * WTM + (slot - TN) * 32, ksn, lane);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
