@@ -46,6 +46,12 @@ MTK_ERR_OOM = -5
 MTK_ERR_LAUNCH = -6
 MTK_ERR_HIP = -7
 
+# GEMM split-K scheduling (mtk_gemm_desc.split_mode); the result is the same bit for bit
+MTK_SPLIT_AUTO = 0
+MTK_SPLIT_TWO_PASS = 1
+MTK_SPLIT_SERIAL = 2
+_SPLIT_MODES = {"auto": MTK_SPLIT_AUTO, "two_pass": MTK_SPLIT_TWO_PASS, "serial": MTK_SPLIT_SERIAL}
+
 F16, BF16, F32 = 0, 1, 2
 _DT = {"f16": F16, "bf16": BF16}
 
@@ -67,7 +73,7 @@ class DeviceInfo(ctypes.Structure):
 
 class GemmDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("M", "N", "K", "lda", "ldb", "ldc", "trans_b", "dtype", "has_bias",
-                                            "split_k", "tile", "trans_a")]
+                                            "split_k", "tile", "trans_a", "split_mode")]
 
 
 class GemmArgs(ctypes.Structure):
@@ -355,10 +361,11 @@ class GemmPlan(_Plan):
     _run_fn = "mtk_gemm_run"
 
     def __init__(self, device: Device | None, M, N, K, *, trans_b=True, dtype="f16", has_bias=False, split_k=1,
-                 tile=0, lda=0, ldb=0, ldc=0, trans_a=False):
+                 tile=0, lda=0, ldb=0, ldc=0, trans_a=False, split_mode="auto"):
         self.desc = GemmDesc(M=M, N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, trans_b=1 if trans_b else 0,
                              dtype=_DT[dtype], has_bias=1 if has_bias else 0, split_k=split_k, tile=tile,
-                             trans_a=1 if trans_a else 0)
+                             trans_a=1 if trans_a else 0,
+                             split_mode=_SPLIT_MODES[split_mode] if isinstance(split_mode, str) else split_mode)
         h = ctypes.c_void_p()
         _check(lib().mtk_gemm_plan(device.handle if device else None, ctypes.byref(self.desc), ctypes.byref(h)))
         super().__init__(h)
@@ -434,14 +441,14 @@ class ConvPlan(_Plan):
 # ------------------------------------------------------------------ harness-level calls
 
 def gemm(dev: Device, A, B, bias=None, *, trans_b=True, dtype="f16", split_k=1, tile=0,
-         trans_a=False) -> np.ndarray:
+         trans_a=False, split_mode="auto") -> np.ndarray:
     """matmul.run equivalent: upload, plan, run, read back C (same 16-bit dtype as the inputs).
     A is [M][K], or [K][M] with trans_a; B is [N][K] with trans_b, else [K][N]."""
     A, B = _bits(A), _bits(B)
     K, M = A.shape if trans_a else A.shape[::-1]
     N = B.shape[0] if trans_b else B.shape[1]
     plan = GemmPlan(dev, M, N, K, trans_b=trans_b, dtype=dtype, has_bias=bias is not None, split_k=split_k, tile=tile,
-                    trans_a=trans_a)
+                    trans_a=trans_a, split_mode=split_mode)
     dA, dB = dev.upload(A), dev.upload(B)
     dbias = dev.upload(_bits(bias)) if bias is not None else None
     dC = dev.empty(M * N * 2)

@@ -8,6 +8,11 @@
 
 #include "kargs.h"
 
+// Every code object records the kernel-argument contract it was built against; the runtime
+// refuses to load one whose version differs from its own (a stale build would read its argument
+// blocks and workspaces with the wrong layout).
+extern "C" __attribute__((used)) __device__ const int32_t mtk_kargs_version = MTK_KARGS_VERSION;
+
 namespace mtk {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));

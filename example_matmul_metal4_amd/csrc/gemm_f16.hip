@@ -2,6 +2,7 @@
 //   *_nt_*_d   B [N][K] (the reference's default layout), direct-to-LDS pipeline
 //   *_nn_*_d   B [K][N] (config 1 "C = A.B row-major"), direct-to-LDS + transposed LDS reads
 //   *_tt_*_d, *_tn_*_d   A [K][M] (the reference's transpose.left) with B [N][K] / [K][N]
+//   *_s        split-K with the partitions run in sequence by one workgroup per tile
 //   *_v1       2-byte register-staged fallback for odd leading dimensions
 // plus the split-K second pass.
 #include "tile_direct.hpp"
@@ -11,6 +12,11 @@ using namespace mtk;
 #define DIRECT_KERNEL(NAME, DT, BM, BN, AOP, BOP)                                   \
   extern "C" __global__ void __launch_bounds__(256) NAME(const mtk_tile_args a) { \
     tile_direct<DT, BM, BN, 2, 2, AOP, BOP>(a);                                   \
+  }
+
+#define SERIAL_KERNEL(NAME, DT, BM, BN, AOP, BOP)                                   \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const mtk_tile_args a) { \
+    tile_direct<DT, BM, BN, 2, 2, AOP, BOP, true>(a);                             \
   }
 
 #define TILE_KERNEL(NAME, DT, BM, BN, WM, WN, AK, BKIND, VA, VB)                    \
@@ -26,6 +32,15 @@ DIRECT_KERNEL(mtk_gemm_f16_tt_256x256_d, DT_F16, 256, 256, OpColsT<256>, OpRows<
 DIRECT_KERNEL(mtk_gemm_f16_tt_128x128_d, DT_F16, 128, 128, OpColsT<128>, OpRows<128>)
 DIRECT_KERNEL(mtk_gemm_f16_tn_256x256_d, DT_F16, 256, 256, OpColsT<256>, OpColsT<256>)
 DIRECT_KERNEL(mtk_gemm_f16_tn_128x128_d, DT_F16, 128, 128, OpColsT<128>, OpColsT<128>)
+
+SERIAL_KERNEL(mtk_gemm_f16_nt_256x256_s, DT_F16, 256, 256, OpRows<256>, OpRows<256>)
+SERIAL_KERNEL(mtk_gemm_f16_nt_128x128_s, DT_F16, 128, 128, OpRows<128>, OpRows<128>)
+SERIAL_KERNEL(mtk_gemm_f16_nn_256x256_s, DT_F16, 256, 256, OpRows<256>, OpColsT<256>)
+SERIAL_KERNEL(mtk_gemm_f16_nn_128x128_s, DT_F16, 128, 128, OpRows<128>, OpColsT<128>)
+SERIAL_KERNEL(mtk_gemm_f16_tt_256x256_s, DT_F16, 256, 256, OpColsT<256>, OpRows<256>)
+SERIAL_KERNEL(mtk_gemm_f16_tt_128x128_s, DT_F16, 128, 128, OpColsT<128>, OpRows<128>)
+SERIAL_KERNEL(mtk_gemm_f16_tn_256x256_s, DT_F16, 256, 256, OpColsT<256>, OpColsT<256>)
+SERIAL_KERNEL(mtk_gemm_f16_tn_128x128_s, DT_F16, 128, 128, OpColsT<128>, OpColsT<128>)
 
 TILE_KERNEL(mtk_gemm_f16_nt_256x256_v1, DT_F16, 256, 256, 2, 2, A_MK, B_NK, 1, 1)
 TILE_KERNEL(mtk_gemm_f16_nt_128x128_v1, DT_F16, 128, 128, 2, 2, A_MK, B_NK, 1, 1)

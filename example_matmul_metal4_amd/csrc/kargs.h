@@ -9,7 +9,7 @@
 
 #include <stdint.h>
 
-#define MTK_KARGS_VERSION 2
+#define MTK_KARGS_VERSION 3
 
 /* Tile-GEMM kernels: plain GEMM (A [M][K] . B, B either [N][K] or [K][N]) and
  * implicit-GEMM convolution (A = im2col of an NDHWC activation, B = DHWIO
@@ -19,7 +19,9 @@ typedef struct {
   const void *B;    /* [N][ldb] (NK) or [K][ldb] (KN) */
   const void *bias; /* [N] or NULL */
   void *C;          /* [M][ldc] output (f16/bf16), or NULL when writing partials */
-  float *partial;   /* [split_k][M][N] fp32 partials, or NULL for the direct epilogue */
+  float *partial;   /* two-pass split-K: [split_k][M][N] fp32 partials (C NULL);
+                       in-workgroup split-K (*_s kernels): [tiles][split_k-1][BM*BN] parked
+                       partition sums (C set); else NULL */
   int32_t M, N, K;
   int32_t lda, ldb, ldc;
   uint32_t a_bytes, b_bytes; /* buffer-resource ranges: loads at or past these byte offsets return 0 */

@@ -101,6 +101,7 @@ struct mtk_plan {
   mtk_conv_desc conv{};
   std::vector<Launch> launches;
   size_t workspace = 0;
+  bool serial_split = false;          // GEMM split-K run in-workgroup (C written by the main kernel)
   unsigned align_a = 2, align_b = 2;  // required operand alignments (bytes)
   double flops = 0, bytes = 0;
   std::string description;
@@ -186,6 +187,8 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   if (d.ldc < d.N) return fail(MTK_ERR_INVALID, "ldc (%d) < N (%d)", d.ldc, d.N);
   if (d.split_k < 0) return fail(MTK_ERR_INVALID, "split_k must be >= 0");
   if (d.tile != 0 && d.tile != 128 && d.tile != 256) return fail(MTK_ERR_INVALID, "tile must be 0, 128 or 256");
+  if (d.split_mode < MTK_SPLIT_AUTO || d.split_mode > MTK_SPLIT_SERIAL)
+    return fail(MTK_ERR_INVALID, "split_mode must be MTK_SPLIT_AUTO, MTK_SPLIT_TWO_PASS or MTK_SPLIT_SERIAL");
   // Buffer ranges end on a whole dword: raw buffer loads range-check per dword, so a last element
   // in the low half of a straddling dword would read as zero. The at most 2 extra bytes lie in the
   // same aligned dword (same page) as the operand's last element; they are masked in the kernels.
@@ -273,13 +276,32 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   const bool direct = d.lda % 2 == 0 && d.ldb % 2 == 0;
   p->align_a = p->align_b = direct ? 4 : 2;
 
+  // Split-K scheduling. In-workgroup ("serial"): one workgroup per tile walks the partitions in
+  // sequence and parks split-1 fp32 partition sums per tile; worth it when the tile grid alone
+  // fills the device (every CU busy without extra partition workgroups), and it saves the second
+  // kernel and 1/split of the partial traffic.
+  bool serial = false;
+  if (split > 1) {
+    const int cus = ctx ? ctx->prop.multiProcessorCount : 256;
+    if (d.split_mode == MTK_SPLIT_SERIAL) {
+      if (split > 4 || !direct) {
+        delete p;
+        return fail(MTK_ERR_UNSUPPORTED, "in-workgroup split-K needs split_k <= 4 and even leading dimensions");
+      }
+      serial = true;
+    } else if (d.split_mode == MTK_SPLIT_AUTO) {
+      serial = direct && split <= 4 && tiles * 4 >= 3LL * cus;
+    }
+  }
+  p->serial_split = serial;
+
   Launch g;
   char name[96];
   // operand letters: A [M][K] 'n' / [K][M] 't', B [N][K] 't' / [K][N] 'n'
   snprintf(name, sizeof name, "mtk_gemm_%s_%c%c_%dx%d_%s", dt, d.trans_a ? 't' : 'n', d.trans_b ? 't' : 'n', tile, tile,
-           direct ? "d" : "v1");
+           serial ? "s" : direct ? "d" : "v1");
   g.name = name;
-  g.grid = (unsigned)(tiles * split);
+  g.grid = (unsigned)(serial ? tiles : tiles * split);
   mtk_tile_args a{};
   a.M = d.M;
   a.N = d.N;
@@ -297,7 +319,9 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   a.has_bias = d.has_bias ? 1 : 0;
   set_args(g, a);
   p->launches.push_back(g);
-  if (split > 1) {
+  if (serial) {
+    p->workspace = (size_t)tiles * (split - 1) * tile * tile * sizeof(float);
+  } else if (split > 1) {
     p->workspace = (size_t)split * d.M * d.N * sizeof(float);
     Launch r;
     r.role = ROLE_REDUCE;
@@ -318,7 +342,7 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   snprintf(desc, sizeof desc, "gemm %s %s %s M=%d N=%d K=%d tile=%dx%d split_k=%d k_tiles/split=%d %s grid=%u%s",
            dt, d.trans_a ? "A[K][M]" : "A[M][K]", d.trans_b ? "B[N][K]" : "B[K][N]", d.M, d.N, d.K, tile, tile, split, kps,
            direct ? "direct-to-LDS" : "2-byte loads", g.grid,
-           split > 1 ? " + splitk_reduce" : "");
+           serial ? " (partitions in sequence per tile, summed in the epilogue)" : split > 1 ? " + splitk_reduce" : "");
   p->description = desc;
   int s = resolve(p);
   if (s != MTK_OK) {
@@ -549,15 +573,15 @@ int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
       k.C = g->C;
       return MTK_OK;
     }
-    const bool split = p->workspace != 0;
+    const bool two_pass = p->workspace != 0 && !p->serial_split;
     for (Launch &l : ls) {
       if (l.role == ROLE_MAIN) {
         mtk_tile_args &a = args_of<mtk_tile_args>(l);
         a.A = g->A;
         a.B = g->B;
         a.bias = g->bias;
-        a.C = split ? nullptr : g->C;
-        a.partial = split ? (float *)g->workspace : nullptr;
+        a.C = two_pass ? nullptr : g->C;
+        a.partial = p->workspace ? (float *)g->workspace : nullptr;
       } else if (l.role == ROLE_REDUCE) {
         mtk_reduce_args &r = args_of<mtk_reduce_args>(l);
         r.partial = (const float *)g->workspace;
@@ -712,6 +736,18 @@ int mtk_init(int device, const char *code_object_dir, mtk_ctx **out) {
     if (e != hipSuccess) {
       (void)hipGetLastError();
       return bail(fail(MTK_ERR_MODULE, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e)));
+    }
+    // the code object's kernel-argument contract must be this library's
+    hipDeviceptr_t gp = nullptr;
+    size_t gsz = 0;
+    int32_t version = -1;
+    e = hipModuleGetGlobal(&gp, &gsz, m, "mtk_kargs_version");
+    if (e == hipSuccess && gsz == sizeof version) e = hipMemcpyDtoH(&version, gp, sizeof version);
+    if (e != hipSuccess || gsz != sizeof version || version != MTK_KARGS_VERSION) {
+      (void)hipGetLastError();
+      (void)hipModuleUnload(m);
+      return bail(fail(MTK_ERR_MODULE, "%s was built for kernel-argument version %d, this library uses %d: rebuild it",
+                       path.c_str(), version, MTK_KARGS_VERSION));
     }
     ctx->modules.push_back(m);
   }

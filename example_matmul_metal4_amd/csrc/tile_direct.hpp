@@ -193,7 +193,13 @@ struct OpColsT {
 
 // ---------------------------------------------------------------- the kernel body
 
-template <int DT, int BM, int BN, int WAVES_M, int WAVES_N, typename AOP, typename BOP>
+// SERIAL (GEMM split-K on a tile grid that already fills the chip, at most 4 partitions): one
+// workgroup per output tile runs the K partitions one after another through one continuous
+// pipeline. At the end of each partition but the last its fp32 sum is parked in the workspace and
+// the accumulators restart from zero; the epilogue adds the parked sums and the last one, then the
+// bias. The arithmetic is the two-pass split-K's: every partition accumulates from zero over the
+// same K-tiles, partition sums are added in partition order, the bias last.
+template <int DT, int BM, int BN, int WAVES_M, int WAVES_N, typename AOP, typename BOP, bool SERIAL = false>
 __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   static_assert(WAVES_M * WAVES_N == 4, "4 wavefronts per workgroup");
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
@@ -218,7 +224,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
 
   const int tiles = a.tiles_m * a.tiles_n;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int split = id / tiles;
+  const int split = SERIAL ? 0 : id / tiles;
   const int t = id - split * tiles;
   const int group = kGroupM * a.tiles_n;
   const int first_m = (t / group) * kGroupM;
@@ -226,8 +232,8 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   const int tm = first_m + (t % group) % gm;
   const int tn = (t % group) / gm;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kt0 = split * a.k_tiles_per_split;
-  const int kt1 = min(kt0 + a.k_tiles_per_split, a.k_tiles);
+  const int kt0 = SERIAL ? 0 : split_first_tile(a, split);
+  const int kt1 = SERIAL ? a.k_tiles : split_first_tile(a, split + 1);
   constexpr bool kAnyTail = AOP::kNeedsTail || BOP::kNeedsTail;
   const bool tail_here = kAnyTail && (a.K % kBK) != 0 && kt1 == a.k_tiles && kt0 < kt1;
   const int kfull = tail_here ? kt1 - 1 : kt1;
@@ -259,6 +265,21 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
 
+  // SERIAL: finished partition p (p < split_k-1) of this workgroup's tile is parked in slot p of
+  // the tile's run of split_k-1 slots in the workspace ([tiles][split_k-1][BM*BN] fp32), in
+  // accumulator order (wave, block (i, j), register quad, lane): each lane moves 16 bytes per
+  // instruction, one instruction covers 1 KB of contiguous memory, and only this lane reads back
+  // what it wrote.
+  constexpr uint32_t kSlotBytes = BM * BN * 4;
+  constexpr int kStorePolicy = 16;  // sc1 stores: measured faster than the default policy for the parks
+  const rsrc_t rslot = make_rsrc(SERIAL ? a.partial + (size_t)t * (a.split_k - 1) * (BM * BN) : nullptr,
+                                 SERIAL ? (uint32_t)(a.split_k - 1) * kSlotBytes : 0u);
+  const uint32_t slot_lane = (uint32_t)(wave * (TM * TN * 1024) + lane * 4) * 4u;
+  auto slot_at = [&](int p, int i, int j, int q) {
+    return slot_lane + (uint32_t)p * kSlotBytes + (uint32_t)((i * TN + j) * 4096 + q * 1024);
+  };
+  int split_end = SERIAL ? split_first_tile(a, 1) : 0;  // SERIAL: first K-tile of the next partition
+  int parked = 0;                                           // SERIAL: partitions parked in the workspace
   if (kt0 < kt1) issue_all(smem, kt0);
   wait_vmem();
   __syncthreads();
@@ -272,62 +293,93 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
 #pragma unroll
   for (int j = 0; j < TN; ++j) fb[0][j] = opb.frag(smem + BM * 128, wave_n * WTN + j * 32, 0, lane);
 
-  for (int kt = kt0; kt < kfull; ++kt) {
-    const int cur = (kt - kt0) & 1;
-    char *nxt = smem + (cur ^ 1) * kStage;
-    // The next tile is the partial last K-tile when there is one. Without one, the last iteration
-    // reloads the current tile into the idle stage (L2 hits, never computed) instead of reaching
-    // into another split's K range: branch-free.
-    const int kn = min(kt + 1, kt1 - 1);
-    const char *sa = smem + cur * kStage;
-    const char *sb = sa + BM * 128;
-    typename std::conditional<std::is_same<AOP, OpConv<BM>>::value, typename OpConv<BM>::Tap, int>::type tp{};
-    if constexpr (std::is_same<AOP, OpConv<BM>>::value) tp = opa.tap(a, kn);
-    __builtin_amdgcn_sched_barrier(0);
+  // SERIAL: the K loop runs once per partition (the pipeline carries on across the boundary: the
+  // last K-tile of a partition prefetches the next one's first); the partition sum is parked
+  // between the runs.
+  int kt = kt0;
+  for (;;) {
+    const int kstop = SERIAL ? min(split_end, kfull) : kfull;
+    for (; kt < kstop; ++kt) {
+      const int cur = (kt - kt0) & 1;
+      char *nxt = smem + (cur ^ 1) * kStage;
+      // The next tile is the partial last K-tile when there is one. Without one, the last iteration
+      // reloads the current tile into the idle stage (L2 hits, never computed) instead of reaching
+      // into another split's K range: branch-free.
+      const int kn = min(kt + 1, kt1 - 1);
+      const char *sa = smem + cur * kStage;
+      const char *sb = sa + BM * 128;
+      typename std::conditional<std::is_same<AOP, OpConv<BM>>::value, typename OpConv<BM>::Tap, int>::type tp{};
+      if constexpr (std::is_same<AOP, OpConv<BM>>::value) tp = opa.tap(a, kn);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int c = ks & 1, nx = c ^ 1;
-      constexpr int kLast = kBK / 16 - 1;
-      if (ks == kLast) {
-        // the next tile has landed (own loads: vmcnt; everyone's: barrier) and every wave is done
-        // reading this tile's stage, which the next iteration starts to overwrite
-        wait_vmem();
-        __syncthreads();
-      }
-      // this k-step's fragments read by inline asm (one k-step earlier)
-      if constexpr (AOP::kAsmFrag) lgkm_wait0(fa[c]);
-      if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[c]);
-      const char *ra_ = ks < kLast ? sa : nxt;
-      const char *rb_ = ks < kLast ? sb : nxt + BM * 128;
-      const int ksn = ks < kLast ? ks + 1 : 0;
+      for (int ks = 0; ks < kBK / 16; ++ks) {
+        const int c = ks & 1, nx = c ^ 1;
+        constexpr int kLast = kBK / 16 - 1;
+        if (ks == kLast) {
+          // the next tile has landed (own loads: vmcnt; everyone's: barrier) and every wave is done
+          // reading this tile's stage, which the next iteration starts to overwrite
+          wait_vmem();
+          __syncthreads();
+        }
+        // this k-step's fragments read by inline asm (one k-step earlier)
+        if constexpr (AOP::kAsmFrag) lgkm_wait0(fa[c]);
+        if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[c]);
+        const char *ra_ = ks < kLast ? sa : nxt;
+        const char *rb_ = ks < kLast ? sb : nxt + BM * 128;
+        const int ksn = ks < kLast ? ks + 1 : 0;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
+        for (int i = 0; i < TM; ++i) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa[c][i], fb[c][j], acc[i][j]);
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa[c][i], fb[c][j], acc[i][j]);
 #pragma unroll
-        for (int u = 0; u < kPerGroup; ++u) {
-          const int q = (ks * TM + i) * kPerGroup + u;
-          if (q < PA) {
-            if constexpr (std::is_same<AOP, OpConv<BM>>::value)
-              opa.issue(ra, nxt, q, tp);
-            else
-              opa.issue(ra, nxt, q, kn);
-          } else if (q < PA + PB) {
-            opb.issue(rb, nxt + BM * 128, q - PA, kn);
+          for (int u = 0; u < kPerGroup; ++u) {
+            const int q = (ks * TM + i) * kPerGroup + u;
+            if (q < PA) {
+              if constexpr (std::is_same<AOP, OpConv<BM>>::value)
+                opa.issue(ra, nxt, q, tp);
+              else
+                opa.issue(ra, nxt, q, kn);
+            } else if (q < PA + PB) {
+              opb.issue(rb, nxt + BM * 128, q - PA, kn);
+            }
           }
-        }
-        // The next k-step's first MFMA group needs every B fragment and only A fragment 0, later
-        // groups one more A fragment each: read the B fragments in the first groups, then A.
+          // The next k-step's first MFMA group needs every B fragment and only A fragment 0, later
+          // groups one more A fragment each: read the B fragments in the first groups, then A.
 #pragma unroll
-        for (int u = 0; u < kReadsPerGroup; ++u) {
-          const int slot = i * kReadsPerGroup + u;
-          if (slot < TN)
-            fb[nx][slot] = opb.frag(rb_, wave_n * WTN + slot * 32, ksn, lane);
-          else if (slot < TN + TM)
-            fa[nx][slot - TN] = opa.frag(ra_, wave_m * WTM + (slot - TN) * 32, ksn, lane);
+          for (int u = 0; u < kReadsPerGroup; ++u) {
+            const int slot = i * kReadsPerGroup + u;
+            if (slot < TN)
+              fb[nx][slot] = opb.frag(rb_, wave_n * WTN + slot * 32, ksn, lane);
+            else if (slot < TN + TM)
+              fa[nx][slot - TN] = opa.frag(ra_, wave_m * WTM + (slot - TN) * 32, ksn, lane);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
+    }
+    if constexpr (!SERIAL) {
+      break;
+    } else {
+      // Partition boundaries lie strictly inside K (at most split_k-1 of them); the K loop ends
+      // anywhere else (or at K itself) after the last partition. Only boundaries park, so every
+      // slot written is one of this tile's split_k-1.
+      if (kt != split_end || split_end >= a.k_tiles || parked >= a.split_k - 1) break;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4, f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                                acc[i][j][4 * q + 3]}),
+                rslot, slot_at(parked, i, j, q), 0, kStorePolicy);
+      ++parked;
+      split_end = split_first_tile(a, parked + 1);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
     }
   }
   // The last prefetch (of a tile that is never computed) may still be in flight. Inline-asm reads
@@ -384,7 +436,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     hi = odd ? x1 : recv;
   };
   // Split-K partials: GEMM only (convolution plans never split K).
-  constexpr bool kPartials = !std::is_same<AOP, OpConv<BM>>::value;
+  constexpr bool kPartials = !SERIAL && !std::is_same<AOP, OpConv<BM>>::value;
   if (kPartials && a.partial != nullptr) {
     float *P = a.partial + (size_t)split * a.M * a.N;
     const bool vec = (a.N & 1) == 0;
@@ -423,20 +475,56 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     __syncthreads();  // every wave is done reading the last K-tile's fragments
     char *ct = smem + wave * (WTM * kRowB);
     const uint16_t *bias = (const uint16_t *)a.bias;
+    // SERIAL: the parked partition sums (at most 3) of each accumulator block, loaded one block
+    // ahead and added in partition order in front of the last partition's: ((p0 + p1) + p2) + acc.
+    constexpr int kMaxParked = 3;
+    const int np = SERIAL ? min(parked, kMaxParked) : 0;
+    f32x4 ring[2][kMaxParked][4];
+    auto fetch = [&](int s, int i, int j) {
+#pragma unroll
+      for (int p = 0; p < kMaxParked; ++p)
+        if (p < np) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            ring[s][p][q] =
+                __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rslot, slot_at(p, i, j, q), 0, 0));
+        }
+    };
+    if constexpr (SERIAL) fetch(0, 0, 0);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int own = nw + j * 32 + (odd ? 1 : 0);  // the column this lane's accumulators belong to
       const float bv = (a.has_bias && own < a.N) ? from_bits<DT>(bias[own]) : 0.0f;
       const int cc = col_l + j * 32;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i) {
+        const int b = j * TM + i;  // fetch order
+        float x[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = acc[i][j][r];
+        if constexpr (SERIAL) {
+          if (b + 1 < TM * TN) fetch((b + 1) & 1, (b + 1) % TM, (b + 1) / TM);
+          if (np > 0) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              f32x4 v = ring[b & 1][0][q];
+#pragma unroll
+              for (int p = 1; p < kMaxParked; ++p)
+                if (p < np) v += ring[b & 1][p][q];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) x[4 * q + e] = v[e] + x[4 * q + e];
+            }
+          }
+        }
 #pragma unroll
         for (int r = 0; r < 16; r += 2) {
           float lo, hi;
-          pair(acc[i][j][r] + bv, acc[i][j][r + 1] + bv, lo, hi);
+          pair(x[r] + bv, x[r + 1] + bv, lo, hi);
           const int rr = row_l + i * 32 + 8 * (r >> 2) + (r & 3);
           *(uint32_t *)(ct + rr * kRowB + (((cc >> 3) ^ swz(rr)) << 4) + (cc & 7) * 2) = pack2<DT>(lo, hi);
         }
+        if constexpr (SERIAL) __builtin_amdgcn_sched_barrier(0);
+      }
     }
     uint16_t *C = (uint16_t *)a.C;
     const bool v16 = (a.ldc & 7) == 0 && ((uintptr_t)a.C & 15) == 0;

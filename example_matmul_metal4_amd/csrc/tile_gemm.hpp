@@ -251,6 +251,12 @@ struct ASel<A_CONV_GENERIC, ROWS, V> {
 
 // ---------------------------------------------------------------- the kernel body
 
+// First K-tile of split-K partition s of a tile (s = split_k: one past the last). Every
+// partition is non-empty: the plan picks split_k = ceil(k_tiles / k_tiles_per_split).
+__device__ __forceinline__ int split_first_tile(const mtk_tile_args &a, int s) {
+  return s >= a.split_k ? a.k_tiles : s * a.k_tiles_per_split;
+}
+
 template <int DT, int BM, int BN, int WAVES_M, int WAVES_N, int AKIND, int BKIND, int VA, int VB>
 __device__ __forceinline__ void tile_gemm(const mtk_tile_args &a) {
   static_assert(WAVES_M * WAVES_N == 4, "4 wavefronts per workgroup");
@@ -277,8 +283,8 @@ __device__ __forceinline__ void tile_gemm(const mtk_tile_args &a) {
   const int tm = first_m + (t % group) % gm;
   const int tn = (t % group) / gm;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kt0 = split * a.k_tiles_per_split;
-  const int kt1 = min(kt0 + a.k_tiles_per_split, a.k_tiles);
+  const int kt0 = split_first_tile(a, split);
+  const int kt1 = split_first_tile(a, split + 1);
 
   const rsrc_t ra = make_rsrc(a.A, a.a_bytes);
   const rsrc_t rb = make_rsrc(a.B, a.b_bytes);

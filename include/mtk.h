@@ -106,7 +106,21 @@ int mtk_set_stream(mtk_ctx *ctx, void *hip_stream);
  * split_k: 1 = none; >1 = that many K partitions with fp32 partials, summed in partition order
  * with the bias added last (the reference's reduce_sum_2, matmul.swift:298-311, 451-474, without
  * its in-place race); 0 = let the plan choose.
- * tile: 0 = let the plan choose; else 128 or 256 (square MFMA workgroup tile). */
+ * tile: 0 = let the plan choose; else 128 or 256 (square MFMA workgroup tile).
+ * split_mode (split_k > 1): how the partitions are scheduled; the arithmetic, and so the result,
+ * is the same bit for bit:
+ *   MTK_SPLIT_AUTO     in-workgroup when the tile grid fills the device and split_k <= 4,
+ *                      else two-pass;
+ *   MTK_SPLIT_TWO_PASS every partition its own workgroup writing fp32 partials [split_k][M][N],
+ *                      then a second kernel sums them and adds the bias (the reference's
+ *                      dispatch, matmul.swift:439-474);
+ *   MTK_SPLIT_SERIAL   one workgroup per output tile runs the partitions in sequence, parks the
+ *                      first split_k-1 partition sums in the workspace and adds them and the bias
+ *                      in its epilogue: no second kernel, (split_k-1)/split_k of the partial
+ *                      traffic (split_k <= 4). */
+#define MTK_SPLIT_AUTO 0
+#define MTK_SPLIT_TWO_PASS 1
+#define MTK_SPLIT_SERIAL 2
 typedef struct {
   int M, N, K;
   int lda, ldb, ldc; /* 0 = packed (K or M, K or N, N) */
@@ -115,7 +129,8 @@ typedef struct {
   int has_bias;
   int split_k;
   int tile;
-  int trans_a; /* appended: earlier fields keep their offsets */
+  int trans_a;    /* appended: earlier fields keep their offsets */
+  int split_mode; /* MTK_SPLIT_*; appended */
 } mtk_gemm_desc;
 
 /* Kernel-select. Replaces createSource(...) + makeLibrary + makeFunction(name:constantValues:) +

@@ -41,6 +41,8 @@ def test_code_objects_hold_every_selectable_kernel():
     names = [f"mtk_gemm_{dt}_{lay}_{t}x{t}_{v}" for dt in ("f16", "bf16") for lay in ("nt", "nn") for t in (128, 256)
              for v in ("d", "v1")]
     names += [f"mtk_gemm_{dt}_{lay}_{t}x{t}_d" for dt in ("f16", "bf16") for lay in ("tt", "tn") for t in (128, 256)]
+    names += [f"mtk_gemm_{dt}_{lay}_{t}x{t}_s" for dt in ("f16", "bf16") for lay in ("nt", "nn", "tt", "tn")
+              for t in (128, 256)]
     names += ["mtk_splitk_reduce_f16", "mtk_splitk_reduce_bf16", "mtk_fill_u16", "mtk_skinny_f16", "mtk_skinny_bf16",
               "mtk_skinny_f16_long", "mtk_skinny_bf16_long"]
     names += [f"mtk_attn_fwd_{dt}{c}" for dt in ("f16", "bf16") for c in ("", "_causal")]
@@ -48,6 +50,47 @@ def test_code_objects_hold_every_selectable_kernel():
     names += [f"mtk_conv_f16_gen_128x128_v{v}" for v in (8, 4, 1)]
     missing = [n for n in names if n.encode() not in blobs]
     assert not missing, missing
+
+
+def _kargs_version_header():
+    src = open(os.path.join(os.path.dirname(mtk.__file__), "csrc", "kargs.h")).read()
+    return int(re.search(r"#define MTK_KARGS_VERSION (\d+)", src).group(1))
+
+
+def _elf_symbol_bytes(elf: bytes, name: str, size: int) -> bytes:
+    """Bytes of a defined symbol of a little-endian ELF64 file (section headers + .symtab)."""
+    import struct
+    shoff, = struct.unpack_from("<Q", elf, 0x28)
+    shentsize, shnum, _ = struct.unpack_from("<HHH", elf, 0x3A)
+    secs = [struct.unpack_from("<IIQQQQIIQQ", elf, shoff + i * shentsize) for i in range(shnum)]
+    for sh in secs:
+        if sh[1] != 2:  # SHT_SYMTAB
+            continue
+        strtab = secs[sh[6]]
+        for off in range(sh[4], sh[4] + sh[5], sh[9]):
+            st_name, st_info, st_other, st_shndx, st_value, st_size = struct.unpack_from("<IBBHQQ", elf, off)
+            end = elf.index(b"\0", strtab[4] + st_name)
+            if elf[strtab[4] + st_name:end].decode() == name and 0 < st_shndx < shnum:
+                sec = secs[st_shndx]
+                at = sec[4] + (st_value - sec[3])
+                return elf[at:at + size]
+    raise KeyError(name)
+
+
+def test_code_objects_carry_the_kernel_argument_version(tmp_path):
+    # The runtime refuses a code object whose mtk_kargs_version differs from its own; every build
+    # output carries the version of the kargs.h it was compiled against.
+    import subprocess
+    want = _kargs_version_header()
+    bundler = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "llvm", "bin", "clang-offload-bundler")
+    units = sorted(f for f in os.listdir(mtk.LIB_DIR) if f.endswith(".hsaco"))
+    assert units
+    for f in units:
+        out = tmp_path / (f + ".co")
+        subprocess.run([bundler, "--unbundle", "--type=o", f"--input={os.path.join(mtk.LIB_DIR, f)}",
+                        "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--output={out}"], check=True)
+        got = int.from_bytes(_elf_symbol_bytes(out.read_bytes(), "mtk_kargs_version", 4), "little")
+        assert got == want, (f, got, want)
 
 
 def test_init_without_gpu_reports_no_device(L):
@@ -70,10 +113,23 @@ def test_status_strings(L):
 
 
 def test_gemm_kernel_select_dry():
+    # config 2: 256 tiles fill the device, so split-K 4 runs in-workgroup (one kernel, 3 parked
+    # partition sums per tile); the two-pass schedule on request
     p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4)
     d = p.describe()
-    assert d.endswith("kernels: mtk_gemm_f16_nt_256x256_d mtk_splitk_reduce_f16") and "split_k=4" in d
+    assert d.endswith("kernels: mtk_gemm_f16_nt_256x256_s") and "split_k=4" in d and "grid=256 " in d
+    assert p.workspace_bytes == 256 * 3 * 256 * 256 * 4  # 3 parked partition sums per tile
+    p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4, split_mode="two_pass")
+    d = p.describe()
+    assert d.endswith("kernels: mtk_gemm_f16_nt_256x256_d mtk_splitk_reduce_f16") and "grid=1024 " in d
     assert p.workspace_bytes == 4 * 4096 * 4096 * 4
+    # a small tile grid keeps the two-pass schedule (the partitions are the parallelism)
+    assert "mtk_splitk_reduce_f16" in mtk.GemmPlan(None, 512, 512, 4100, split_k=4).describe()
+    p = mtk.GemmPlan(None, 512, 512, 4100, split_k=4, split_mode="serial")
+    assert p.describe().endswith("kernels: mtk_gemm_f16_nt_128x128_s") and p.workspace_bytes == 16 * 3 * 128 * 128 * 4
+    assert "_tn_256x256_s" in mtk.GemmPlan(None, 4096, 4096, 512, split_k=2, trans_a=True, trans_b=False,
+                                            dtype="bf16").describe()
+    p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4)
     flops, byts = p.work()
     assert flops == 2 * 4096 * 4096 * 4100 and byts == 2 * (4096 * 4100 * 2 + 4096 * 4096 + 4096)
     p = mtk.GemmPlan(None, 256, 256, 256, trans_b=False)
@@ -94,7 +150,7 @@ def test_gemm_kernel_select_dry():
     assert "mtk_skinny_f16_long" in p.describe() and "grid=256 " in p.describe()
     assert "grid=3 " in mtk.GemmPlan(None, 8, 40, 256, split_k=2).describe()
     # transpose.left: A [K][M] through the transposed-read policy; never the skinny path
-    p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4, trans_a=True)
+    p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4, trans_a=True, split_mode="two_pass")
     assert "mtk_gemm_f16_tt_256x256_d" in p.describe() and "A[K][M]" in p.describe()
     assert "mtk_gemm_bf16_tn_128x128_d" in mtk.GemmPlan(None, 16, 64, 64, dtype="bf16", trans_a=True,
                                                           trans_b=False).describe()
@@ -110,6 +166,9 @@ def test_gemm_kernel_select_dry():
     (dict(M=4, N=4, K=8, ldc=2), mtk.MTK_ERR_INVALID),
     (dict(M=4, N=4, K=8, split_k=-2), mtk.MTK_ERR_INVALID),
     (dict(M=4, N=4, K=8, tile=64), mtk.MTK_ERR_INVALID),
+    (dict(M=4, N=4, K=8, split_mode=3), mtk.MTK_ERR_INVALID),
+    (dict(M=64, N=64, K=2048, split_k=8, split_mode="serial"), mtk.MTK_ERR_UNSUPPORTED),
+    (dict(M=64, N=64, K=1024, lda=1025, split_k=2, split_mode="serial"), mtk.MTK_ERR_UNSUPPORTED),
     (dict(M=70000, N=4, K=20000), mtk.MTK_ERR_UNSUPPORTED),
     (dict(M=8, N=4, K=8, trans_a=True, lda=6), mtk.MTK_ERR_INVALID),        # lda < M
     (dict(M=7, N=4, K=8, trans_a=True), mtk.MTK_ERR_UNSUPPORTED),           # odd lda for A [K][M]
