@@ -72,8 +72,9 @@ def time_steps(dev, plan, arg_sets, warmup, steps):
     return wall_ms, eager_ms, prof
 
 
-def gemm_case(dev, mtk, inputs, M, N, K, dtype, split_k, seeds, dists, copies=3, tile=0):
-    plan = mtk.GemmPlan(dev, M, N, K, trans_b=True, dtype=dtype, has_bias=True, split_k=split_k, tile=tile)
+def gemm_case(dev, mtk, inputs, M, N, K, dtype, split_k, seeds, dists, copies=3, tile=0, split_mode="auto"):
+    plan = mtk.GemmPlan(dev, M, N, K, trans_b=True, dtype=dtype, has_bias=True, split_k=split_k, tile=tile,
+                        split_mode=split_mode)
     C = dev.empty(M * N * 2)
     ws = dev.empty(plan.workspace_bytes) if plan.workspace_bytes else None
     sets = []
@@ -211,7 +212,9 @@ def main():
         "dtype": "f16",
         "data": "synthetic (seeded SplitMix64: A,B ~ N(0,1)/sqrt(K), bias ~ U[-0.5,0.5)); 3 rotating input copies",
         "config": {"workload": "BASELINE config 2: fp16 GEMM C = A.B^T + bias, M=N=4096, K=4100, split-K=4, "
-                               "B [N][K], fp32 accumulate, fp16 out",
+                               "B [N][K], fp32 accumulate, fp16 out; split-K run in-workgroup (the 4 K partitions "
+                               "in sequence per output tile, fp32 partition sums parked and added in partition "
+                               "order, bias last: the two-pass schedule's arithmetic, one kernel)",
                    "M": M, "N": N, "K": K, "split_k": 4, "pct_mfma_peak": 100 * value / PEAK_F16_TFLOPS},
         "roofline": {"bound": "mfma", "kernel": gemm_kernel, "achieved": achieved, "peak": PEAK_F16_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic_for(f"{gemm_kernel}@config2_splitk4"),
@@ -228,6 +231,12 @@ def main():
             tm = time_steps(dev, p1, s1, args.warmup, steps)
             cfgs["config2_splitk1"] = summarize("config 2 without split-K (split_k=1)", p1, tm, "mfma",
                                                 key="config2_splitk1")
+            p2, s2 = gemm_case(dev, mtk, inputs, M, N, K, "f16", 4, (1, 2, 3),
+                               (nrm(1 / np.sqrt(K)), nrm(1 / np.sqrt(K)), uni(-0.5, 0.5)), split_mode="two_pass")
+            tm = time_steps(dev, p2, s2, args.warmup, steps)
+            cfgs["config2_splitk4_two_pass"] = summarize(
+                "config 2, split-K 4 in the two-pass schedule (partition workgroups + reduce kernel)", p2, tm, "mfma",
+                key="config2_splitk4_two_pass")
             p3, s3 = gemm_case(dev, mtk, inputs, 16, 14336, 4096, "bf16", 8, (4, 5, 6),
                                (nrm(1.0), nrm(0.02), nrm(0.02)), copies=3)
             tm = time_steps(dev, p3, s3, args.warmup, steps * 4)

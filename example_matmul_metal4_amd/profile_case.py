@@ -3,6 +3,7 @@
 once; only the plan's kernels run in the loop.
 
     python -m example_matmul_metal4_amd.profile_case gemm --split 4 --iters 20
+    python -m example_matmul_metal4_amd.profile_case gemm --split 4 --mode two_pass --iters 20
     python -m example_matmul_metal4_amd.profile_case copy --iters 20   # calibration: plain copy
 
 Cases: gemm (config 2, 4096 x 4096 x 4100 + bias, B [N][K]), gemm_nn (4096^3, B [K][N]), decode
@@ -22,6 +23,8 @@ def main(argv=None):
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--split", type=int, default=4)
     ap.add_argument("--tile", type=int, default=0)
+    ap.add_argument("--mode", choices=["auto", "two_pass", "serial"], default="auto",
+                    help="split-K schedule of the gemm case")
     a = ap.parse_args(argv)
 
     if a.case == "copy":
@@ -45,7 +48,7 @@ def main(argv=None):
         if a.case == "gemm":
             M = N = 4096
             K = 4100
-            plan = mtk.GemmPlan(dev, M, N, K, has_bias=True, split_k=a.split, tile=a.tile)
+            plan = mtk.GemmPlan(dev, M, N, K, has_bias=True, split_k=a.split, tile=a.tile, split_mode=a.mode)
             ws = dev.empty(plan.workspace_bytes) if plan.workspace_bytes else None
             sets = [plan.args(dev.upload(inputs.normal(1, (M, K), 0, 1 / np.sqrt(K))),
                               dev.upload(inputs.normal(2, (N, K), 0, 1 / np.sqrt(K))),
