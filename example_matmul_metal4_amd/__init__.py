@@ -82,7 +82,7 @@ class GemmArgs(ctypes.Structure):
 
 
 class AttnDesc(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_int) for n in ("B", "H", "S_q", "S_kv", "D", "causal", "dtype")]
+    _fields_ = [(n, ctypes.c_int) for n in ("B", "H", "S_q", "S_kv", "D", "causal", "dtype", "q_rows")]
 
 
 class AttnArgs(ctypes.Structure):
@@ -384,8 +384,9 @@ class AttentionPlan(_Plan):
     _args_type = AttnArgs
     _run_fn = "mtk_attn_run"
 
-    def __init__(self, device: Device | None, B, H, S_q, S_kv, D=128, *, causal=False, dtype="f16"):
-        self.desc = AttnDesc(B=B, H=H, S_q=S_q, S_kv=S_kv, D=D, causal=1 if causal else 0, dtype=_DT[dtype])
+    def __init__(self, device: Device | None, B, H, S_q, S_kv, D=128, *, causal=False, dtype="f16", q_rows=0):
+        self.desc = AttnDesc(B=B, H=H, S_q=S_q, S_kv=S_kv, D=D, causal=1 if causal else 0, dtype=_DT[dtype],
+                             q_rows=q_rows)
         h = ctypes.c_void_p()
         _check(lib().mtk_attn_plan(device.handle if device else None, ctypes.byref(self.desc), ctypes.byref(h)))
         super().__init__(h)
@@ -462,11 +463,11 @@ def gemm(dev: Device, A, B, bias=None, *, trans_b=True, dtype="f16", split_k=1, 
     return out
 
 
-def attention(dev: Device, Q, K, V, *, causal=False, dtype="f16") -> np.ndarray:
+def attention(dev: Device, Q, K, V, *, causal=False, dtype="f16", q_rows=0) -> np.ndarray:
     """attention.run equivalent on [B][S][H][D] tensors."""
     Q, K, V = _bits(Q), _bits(K), _bits(V)
     B, Sq, H, D = Q.shape
-    plan = AttentionPlan(dev, B, H, Sq, K.shape[1], D, causal=causal, dtype=dtype)
+    plan = AttentionPlan(dev, B, H, Sq, K.shape[1], D, causal=causal, dtype=dtype, q_rows=q_rows)
     dQ, dK, dV = dev.upload(Q), dev.upload(K), dev.upload(V)
     dO = dev.empty(Q.nbytes)
     plan.run(dQ, dK, dV, dO)

@@ -11,7 +11,7 @@
 //     64 keys, two LDS slots each, filled by direct-to-LDS loads (no register staging).
 //   * Scores are computed transposed on 32x32x16 MFMA: the accumulator column (lane % 32) is the
 //     query, so each lane owns one query and the softmax row max / row sum are in-register
-//     reductions plus one exchange with lane ^ 32.
+//     reductions plus one exchange with lane ^ 32 (v_permlane32_swap, no LDS round trip).
 //   * K rows are fed to the MFMA in a permuted order (MFMA row m reads key swap_bits_2_3(m)); with
 //     that order accumulator register r of lane (i, g = lane/32) holds key 8g + r (r < 8) or
 //     16 + 8g + (r - 8), which is exactly the B-operand layout of the P.V MFMA (O^T = V^T . P^T).
@@ -178,7 +178,7 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
 #pragma unroll
         for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = half_max(mx);
       const float m_tile = mx * c;
       float alpha = 1.0f;
       if (m_tile > m_off + kRescaleSlack) {
@@ -252,7 +252,7 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
   }
 
   // ---- epilogue: O[qi][h][d] = O^T[d][qi] / l
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = half_sum(l_run);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   if (qi < a.S_q) {
     uint16_t *O = (uint16_t *)a.O;
@@ -266,6 +266,273 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
                       pack2<DT>(o[db][4 * rq + 2] * inv, o[db][4 * rq + 3] * inv)};
         *(u32x2 *)(O + obase + d) = v;
       }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Wide-query variant: 64 queries per wavefront (two 32-query blocks), 256 per workgroup, one
+// wavefront per SIMD with the whole register file. Every K fragment read from LDS feeds the S MFMAs
+// of both query blocks and every V^T fragment the P.V MFMAs of both: half the LDS reads per MFMA of
+// the 32-query kernel above, and registers to read fragments further ahead. Same data layout,
+// permutations, lazy rescale and pipeline; the softmax state is kept per query block.
+constexpr int kBQW = 256;
+
+template <int DT, bool CAUSAL>
+__device__ __forceinline__ void attn_fwd_wide(const mtk_attn_kargs &a) {
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTile];  // K slots 0, 1 then V slots 0, 1
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, col = lane & 31;
+
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = id / a.q_blocks;
+  int qb_id = id - bh * a.q_blocks;
+  if (CAUSAL) qb_id = a.q_blocks - 1 - qb_id;  // heaviest query blocks first
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int q0 = qb_id * kBQW;
+  const uint32_t rs = (uint32_t)a.H * kD * 2;
+  const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kD * 2);
+  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H + h) * kD * 2);
+  const rsrc_t rq = make_rsrc(a.Q, a.q_bytes);
+  const rsrc_t rk = make_rsrc(a.K, a.kv_bytes);
+  const rsrc_t rv = make_rsrc(a.V, a.kv_bytes);
+  const int diag = a.S_kv - a.S_q;
+
+  // this lane's two queries (one per query block) as B operands of S^T = K . Q^T
+  int qi[2];
+  u32x4 qf[2][8];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    qi[qb] = q0 + wave * 64 + qb * 32 + col;
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds)
+      qf[qb][ds] =
+          buf_load16(rq, qi[qb] < a.S_q ? qbase + (uint32_t)qi[qb] * rs + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB);
+  }
+
+  int kv_end = a.S_kv;
+  if (CAUSAL) kv_end = min(a.S_kv, q0 + kBQW + diag);
+  const int n_tiles = kv_end > 0 ? (kv_end + kBKV - 1) / kBKV : 0;
+
+  int srow[4];
+  uint32_t kcol[4], vcol[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    srow[i] = (wave * 4 + i) * 4 + (lane >> 4);
+    const int pc = lane & 15;
+    kcol[i] = 16u * (uint32_t)(pc ^ (srow[i] & 15));
+    vcol[i] = 16u * (uint32_t)(pc ^ (4 * (srow[i] & 3)));
+  }
+  auto issue_k = [&](int slot, int t) {
+    char *dst = smem + slot * kTile + wave * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = t * kBKV + srow[i];
+      lds_direct16(rk, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + kcol[i] : kOOB);
+    }
+  };
+  auto issue_v = [&](int slot, int t) {
+    char *dst = smem + (2 + slot) * kTile + wave * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = t * kBKV + srow[i];
+      lds_direct16(rv, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + vcol[i] : kOOB);
+    }
+  };
+
+  const int krow = swap_bits_2_3(col);
+  auto kfrag = [&](const char *kt, int blk, int ds) -> u32x4 {
+    return *(const u32x4 *)(kt + k_off(krow + 32 * blk, 2 * ds + g));
+  };
+  const int vs = lane & 15, vh = lane >> 4;
+  auto vfrag = [&](const char *vt, int db, int js) -> u32x4 {
+    const int d = 32 * db + 16 * (vh & 1) + 4 * (vs & 3);
+    u32x4 v;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int row = 16 * js + 8 * (vh >> 1) + 4 * e + (vs >> 2);
+      const u32x2 w = ds_read_tr16(vt + row * 256 + 16 * ((d >> 3) ^ (4 * (row & 3))) + 2 * (d & 7));
+      v[2 * e] = w.x;
+      v[2 * e + 1] = w.y;
+    }
+    return v;
+  };
+
+  float m_off[2] = {-INFINITY, -INFINITY};  // exponent offset per query block (log2 domain)
+  float l_run[2] = {0.0f, 0.0f};            // this lane's half of the running row sums
+  f32x16 o[2][4];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[qb][i] = f32x16{};
+  const float c = a.scale_log2;
+  const int wave_q_min = q0 + wave * 64;
+
+  if (n_tiles > 0) {
+    f32x16 s[2][2];  // [key block][query block]: S^T of the tile being softmaxed
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) s[kb][qb] = f32x16{};
+    issue_k(0, 0);
+    wait_vmem();
+    __syncthreads();
+    if (n_tiles > 1) issue_k(1, 1);
+    issue_v(0, 0);
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const u32x4 kf = kfrag(smem, kb, ds);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) s[kb][qb] = mfma32x32x16<DT>(kf, qf[qb][ds], s[kb][qb]);
+      }
+    float mx[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      mx[qb] = fmaxf(s[0][qb][0], s[1][qb][0]);
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx[qb] = fmaxf(mx[qb], fmaxf(s[0][qb][r], s[1][qb][r]));
+    }
+
+    for (int t = 0; t < n_tiles; ++t) {
+      wait_vmem();
+      __syncthreads();  // K(t+1) and V(t) are in LDS; K slot t&1 and V slot (t+1)&1 are free
+      if (t + 2 < n_tiles) issue_k(t & 1, t + 2);
+      if (t + 1 < n_tiles) issue_v((t + 1) & 1, t + 1);
+      const char *kn = smem + ((t + 1) & 1) * kTile;
+      const char *vt = smem + (2 + (t & 1)) * kTile;
+      // K(t+1) fragments of the first two k-steps: read now, consumed after the softmax
+      // bookkeeping below; later k-steps are read two k-steps ahead inside phase A
+      u32x4 kf[8][2];
+#pragma unroll
+      for (int ds = 0; ds < 2; ++ds)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) kf[ds][kb] = kfrag(kn, kb, ds);
+
+      const int j0 = t * kBKV;
+      if ((j0 + kBKV > a.S_kv) || (CAUSAL && j0 + kBKV - 1 > wave_q_min + diag)) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int kr0 = (r < 8) ? (8 * g + r) : (16 + 8 * g + (r - 8));
+            const int key0 = j0 + kr0, key1 = j0 + 32 + kr0;
+            s[0][qb][r] = (key0 < a.S_kv && (!CAUSAL || key0 <= qi[qb] + diag)) ? s[0][qb][r] : -INFINITY;
+            s[1][qb][r] = (key1 < a.S_kv && (!CAUSAL || key1 <= qi[qb] + diag)) ? s[1][qb][r] : -INFINITY;
+          }
+          mx[qb] = fmaxf(s[0][qb][0], s[1][qb][0]);
+#pragma unroll
+          for (int r = 1; r < 16; ++r) mx[qb] = fmaxf(mx[qb], fmaxf(s[0][qb][r], s[1][qb][r]));
+        }
+      }
+      float moff[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float m = half_max(mx[qb]);
+        const float m_tile = m * c;
+        float alpha = 1.0f;
+        if (m_tile > m_off[qb] + kRescaleSlack) {
+          alpha = __builtin_amdgcn_exp2f(m_off[qb] - m_tile);
+          m_off[qb] = m_tile;
+        }
+        moff[qb] = m_off[qb] == -INFINITY ? 0.0f : m_off[qb];
+        l_run[qb] *= alpha;
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[qb][i] *= alpha;
+        }
+      }
+
+      // phase A: S(t+1) MFMAs (each K fragment feeds both query blocks) interleaved with the
+      // exponentials / sums / packing of tile t
+      f32x16 n[2][2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) n[kb][qb] = f32x16{};
+      u32x4 pf[2][4];
+      float psum[2] = {0.0f, 0.0f};
+      u32x4 vf[2][4];
+#pragma unroll
+      for (int ds = 0; ds < 8; ++ds) {
+        if (ds + 2 < 8) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) kf[ds + 2][kb] = kfrag(kn, kb, ds + 2);
+        } else {
+          // the first d block's V^T fragments for phase B (V(t) is in LDS since the barrier)
+#pragma unroll
+          for (int js = 2 * (ds - 6); js < 2 * (ds - 6) + 2; ++js) vf[0][js] = vfrag(vt, 0, js);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) n[kb][qb] = mfma32x32x16<DT>(kf[ds][kb], qf[qb][ds], n[kb][qb]);
+        const int r = 2 * ds;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          const float p00 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[0][qb][r], c, -moff[qb]));
+          const float p01 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[0][qb][r + 1], c, -moff[qb]));
+          const float p10 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[1][qb][r], c, -moff[qb]));
+          const float p11 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[1][qb][r + 1], c, -moff[qb]));
+          psum[qb] += (p00 + p01) + (p10 + p11);
+          pf[qb][r >> 3][(r & 7) >> 1] = pack2<DT>(p00, p01);
+          pf[qb][2 + (r >> 3)][(r & 7) >> 1] = pack2<DT>(p10, p11);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      l_run[0] += psum[0];
+      l_run[1] += psum[1];
+
+      // phase B: O^T += V^T(t) . P^T(t) for both query blocks, interleaved with the row maxima of
+      // S(t+1); the next d block's V^T fragments are read while the current block's MFMAs run
+      float mn[2] = {fmaxf(n[0][0][0], n[1][0][0]), fmaxf(n[0][1][0], n[1][1][0])};
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int cb = db & 1, nb = cb ^ 1;
+        lgkm_wait0(vf[cb]);
+        if (db + 1 < 4) {
+#pragma unroll
+          for (int js = 0; js < 4; ++js) vf[nb][js] = vfrag(vt, db + 1, js);
+        }
+#pragma unroll
+        for (int js = 0; js < 4; ++js)
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) o[qb][db] = mfma32x32x16<DT>(vf[cb][js], pf[qb][js], o[qb][db]);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int r = 4 * db; r < 4 * db + 4; ++r) mn[qb] = fmaxf(mn[qb], fmaxf(n[0][qb][r], n[1][qb][r]));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) s[kb][qb] = n[kb][qb];
+      mx[0] = mn[0];
+      mx[1] = mn[1];
+    }
+  }
+
+  // ---- epilogue: O[qi][h][d] = O^T[d][qi] / l, per query block
+  uint16_t *O = (uint16_t *)a.O;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float l_tot = half_sum(l_run[qb]);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (qi[qb] < a.S_q) {
+      const size_t obase = (((size_t)b * a.S_q + qi[qb]) * a.H + h) * kD;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int d = db * 32 + 8 * rq + 4 * g;
+          const u32x2 v{pack2<DT>(o[qb][db][4 * rq + 0] * inv, o[qb][db][4 * rq + 1] * inv),
+                        pack2<DT>(o[qb][db][4 * rq + 2] * inv, o[qb][db][4 * rq + 3] * inv)};
+          *(u32x2 *)(O + obase + d) = v;
+        }
+    }
   }
 }
 
@@ -283,3 +550,14 @@ ATTN_KERNEL(mtk_attn_fwd_f16, DT_F16, false)
 ATTN_KERNEL(mtk_attn_fwd_bf16, DT_BF16, false)
 ATTN_KERNEL(mtk_attn_fwd_f16_causal, DT_F16, true)
 ATTN_KERNEL(mtk_attn_fwd_bf16_causal, DT_BF16, true)
+
+#define ATTN_WIDE_KERNEL(NAME, DT, CAUSAL)                                                             \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))        \
+  NAME(const mtk_attn_kargs a) {                                                                       \
+    attn_fwd_wide<DT, CAUSAL>(a);                                                                      \
+  }
+
+ATTN_WIDE_KERNEL(mtk_attn_fwd_w_f16, DT_F16, false)
+ATTN_WIDE_KERNEL(mtk_attn_fwd_w_bf16, DT_BF16, false)
+ATTN_WIDE_KERNEL(mtk_attn_fwd_w_f16_causal, DT_F16, true)
+ATTN_WIDE_KERNEL(mtk_attn_fwd_w_bf16_causal, DT_BF16, true)

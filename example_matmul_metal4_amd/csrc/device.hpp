@@ -155,6 +155,28 @@ __device__ __forceinline__ void lgkm_wait0(u32x4 (&f)[N]) {
 // Workgroup id remap so that consecutive logical ids share an XCD: hardware hands
 // workgroup b to XCD (b % 8); XCD x receives its ids in order, so logical id =
 // (ids owned by XCDs before x) + (b / 8). A bijection on [0, n).
+// Combine a lane's value with lane ^ 32's without going through LDS (v_permlane32_swap: the two
+// halves of the wave trade places). Both halves compute (lower half's value) op (upper half's), so
+// they get identical results. The elements are copied to scalars before the bit casts (see the
+// note on __builtin_bit_cast above).
+__device__ __forceinline__ void half_swap(float x, float &lo, float &hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  const uint32_t r0 = r[0], r1 = r[1];  // lanes < 32: (x, x[lane + 32]); lanes >= 32: (x[lane - 32], x)
+  lo = __builtin_bit_cast(float, r0);
+  hi = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float half_max(float x) {
+  float lo, hi;
+  half_swap(x, lo, hi);
+  return fmaxf(lo, hi);
+}
+__device__ __forceinline__ float half_sum(float x) {
+  float lo, hi;
+  half_swap(x, lo, hi);
+  return lo + hi;
+}
+
 __device__ __forceinline__ int xcd_remap(int b, int n) {
   const int q = n >> 3, r = n & 7, x = b & 7;
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + (b >> 3);

@@ -497,14 +497,14 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
 
 // ------------------------------------------------------------------ attention planning
 
-constexpr int kAttnRowsPerWG = 128;  // query rows per workgroup (4 waves x 32)
-
 int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   if (!d_in || !out) return fail(MTK_ERR_INVALID, "null descriptor or output");
   mtk_attn_desc d = *d_in;
   if (d.B <= 0 || d.H <= 0 || d.S_q <= 0 || d.S_kv <= 0) return fail(MTK_ERR_INVALID, "B, H, S_q, S_kv must be positive");
   if (d.D != 128) return fail(MTK_ERR_UNSUPPORTED, "head dimension must be 128 (got %d)", d.D);
   if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "attention dtype must be MTK_F16 or MTK_BF16");
+  if (d.q_rows != 0 && d.q_rows != 128 && d.q_rows != 256)
+    return fail(MTK_ERR_INVALID, "q_rows must be 0, 128 or 256 (got %d)", d.q_rows);
   const uint64_t q_bytes = (uint64_t)d.B * d.S_q * d.H * d.D * 2;
   const uint64_t kv_bytes = (uint64_t)d.B * d.S_kv * d.H * d.D * 2;
   if (q_bytes > kMaxOperandBytes || kv_bytes > kMaxOperandBytes)
@@ -514,14 +514,19 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   p->kind = PLAN_ATTN;
   p->attn = d;
   p->align_a = p->align_b = 16;
+  // Query rows per workgroup: 128 (two workgroups, 8 wavefronts per CU) unless asked for. The
+  // 256-row kernel (one wavefront per SIMD, half the LDS reads per MFMA) measures slower at every
+  // size tried: with one wavefront per SIMD nothing hides its stalls.
+  const int rows = d.q_rows ? d.q_rows : 128;
   Launch g;
-  g.name = std::string("mtk_attn_fwd_") + (d.dtype == MTK_F16 ? "f16" : "bf16") + (d.causal ? "_causal" : "");
+  g.name = std::string("mtk_attn_fwd_") + (rows == 256 ? "w_" : "") + (d.dtype == MTK_F16 ? "f16" : "bf16") +
+           (d.causal ? "_causal" : "");
   mtk_attn_kargs a{};
   a.B = d.B;
   a.H = d.H;
   a.S_q = d.S_q;
   a.S_kv = d.S_kv;
-  a.q_blocks = (d.S_q + kAttnRowsPerWG - 1) / kAttnRowsPerWG;
+  a.q_blocks = (d.S_q + rows - 1) / rows;
   a.causal = d.causal ? 1 : 0;
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)d.D));
   a.q_bytes = (uint32_t)q_bytes;
@@ -541,7 +546,7 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   p->bytes = 2.0 * (double)q_bytes + 2.0 * (double)kv_bytes;
   char desc[256];
   snprintf(desc, sizeof desc, "attention fwd %s B=%d H=%d S_q=%d S_kv=%d D=%d causal=%d rows/wg=%d grid=%u",
-           d.dtype == MTK_F16 ? "f16" : "bf16", d.B, d.H, d.S_q, d.S_kv, d.D, d.causal, kAttnRowsPerWG, g.grid);
+           d.dtype == MTK_F16 ? "f16" : "bf16", d.B, d.H, d.S_q, d.S_kv, d.D, d.causal, rows, g.grid);
   p->description = desc;
   int s = resolve(p);
   if (s != MTK_OK) {

@@ -153,11 +153,14 @@ int mtk_gemm_run(const mtk_plan *plan, const mtk_gemm_args *args);
  * constants (Sources/attention/attention.swift:9-21, 117-120, 423-431).
  * Q, O: [B][S_q][H][D]; K, V: [B][S_kv][H][D] (the reference's [S][H][D] packing,
  * attention.swift:466-468, with a batch dimension). D must be 128. scale = 1/sqrt(D).
- * causal != 0 keeps keys j <= i + (S_kv - S_q) for query i (bottom-right aligned). */
+ * causal != 0 keeps keys j <= i + (S_kv - S_q) for query i (bottom-right aligned).
+ * q_rows: query rows per workgroup, 0 = let the plan choose; 128 (32 per wavefront, two
+ * workgroups per CU) or 256 (64 per wavefront, one workgroup per CU: half the LDS reads per MFMA). */
 typedef struct {
   int B, H, S_q, S_kv, D;
   int causal;
-  int dtype; /* MTK_F16 (MTK_BF16 accepted) */
+  int dtype;  /* MTK_F16 (MTK_BF16 accepted) */
+  int q_rows; /* appended: earlier fields keep their offsets */
 } mtk_attn_desc;
 
 /* Replaces createSource(blockDimensions:attentionDimensions:buildOptions:) + pipeline setup

@@ -29,9 +29,9 @@ def probs_f64(Q, K, causal, dtype="f16"):
     return np.where(den > 0, p / np.where(den > 0, den, 1), 0.0)
 
 
-def check(dev, Q, K, V, causal, dtype="f16", label=""):
-    print(f"[attn] {label} Q{Q.shape} Skv={K.shape[1]} causal={causal} {dtype}", flush=True)
-    got = mtk.attention(dev, Q, K, V, causal=causal, dtype=dtype)
+def check(dev, Q, K, V, causal, dtype="f16", label="", q_rows=0):
+    print(f"[attn] {label} Q{Q.shape} Skv={K.shape[1]} causal={causal} {dtype} q_rows={q_rows}", flush=True)
+    got = mtk.attention(dev, Q, K, V, causal=causal, dtype=dtype, q_rows=q_rows)
     exp = oracle.attention(Q, K, V, causal=causal, dtype=dtype)
     p = probs_f64(Q, K, causal, dtype)
     absv = np.abs(oracle.to_f32(V, dtype).astype(np.float64))
@@ -62,40 +62,50 @@ def test_fixtures(dev, golden_dir):
         assert oracle.compare(got.astype(np.float32), fx[key])["ok"]
 
 
-@pytest.mark.parametrize("S", [1, 7, 31, 64, 65, 127, 128, 129, 257, 511, 1000, 1023])
+# query rows per workgroup: 128 (32 per wavefront) and 256 (64 per wavefront) kernels
+ROWS = [128, 256]
+
+
+@pytest.mark.parametrize("S", [1, 7, 31, 64, 65, 127, 128, 129, 255, 257, 511, 1000, 1023])
 @pytest.mark.parametrize("causal", [False, True])
-def test_sequence_sweep(dev, S, causal):
+@pytest.mark.parametrize("q_rows", ROWS)
+def test_sequence_sweep(dev, S, causal, q_rows):
     # mirrors profileCorrectness (attention.swift:391-396): S = 1..1023, D = 128, H = 8
     Q, K, V = qkv(1000 + S, 1, S, 8)
-    check(dev, Q, K, V, causal, label=f"S{S}")
+    check(dev, Q, K, V, causal, label=f"S{S}", q_rows=q_rows)
 
 
-@pytest.mark.parametrize("sq,skv", [(100, 300), (300, 100), (64, 1)])
+@pytest.mark.parametrize("sq,skv", [(100, 300), (300, 100), (64, 1), (700, 260)])
 @pytest.mark.parametrize("causal", [False, True])
-def test_unequal_lengths(dev, sq, skv, causal):
+@pytest.mark.parametrize("q_rows", ROWS)
+def test_unequal_lengths(dev, sq, skv, causal, q_rows):
     Q, K, V = qkv(77, 2, sq, 3, Skv=skv)
-    check(dev, Q, K, V, causal, label=f"{sq}x{skv}")
+    check(dev, Q, K, V, causal, label=f"{sq}x{skv}", q_rows=q_rows)
 
 
 @pytest.mark.parametrize("causal", [False, True])
-def test_bf16(dev, causal):
+@pytest.mark.parametrize("q_rows", ROWS)
+def test_bf16(dev, causal, q_rows):
     Q, K, V = qkv(5, 2, 333, 4, dtype="bf16")
-    check(dev, Q, K, V, causal, dtype="bf16", label="bf16")
+    check(dev, Q, K, V, causal, dtype="bf16", label="bf16", q_rows=q_rows)
 
 
-def test_closed_forms(dev):
-    B, S, H = 1, 200, 2
+@pytest.mark.parametrize("q_rows", ROWS)
+def test_closed_forms(dev, q_rows):
+    B, S, H = 1, 300, 2
     Q, K, _ = qkv(9, B, S, H)
     row = oracle.normal(12, (1, 1, H, 128))
     Vc = np.broadcast_to(row, (B, S, H, 128)).copy()
-    O = mtk.attention(dev, Q, K, Vc)  # constant V rows -> O = that row
+    O = mtk.attention(dev, Q, K, Vc, q_rows=q_rows)  # constant V rows -> O = that row
     assert np.allclose(O.astype(np.float32), np.broadcast_to(row.astype(np.float32), O.shape), atol=2e-3, rtol=1e-3)
     V = oracle.normal(13, (B, S, H, 128))
-    O = mtk.attention(dev, np.zeros_like(Q), K, V, causal=True)  # Q = 0 -> prefix means
+    O = mtk.attention(dev, np.zeros_like(Q), K, V, causal=True, q_rows=q_rows)  # Q = 0 -> prefix means
     pref = np.cumsum(V.astype(np.float64), 1) / np.arange(1, S + 1)[None, :, None, None]
     assert np.allclose(O.astype(np.float64), pref, atol=3e-3)
-    O = mtk.attention(dev, Q, K, V, causal=True)  # first query sees only key 0
+    O = mtk.attention(dev, Q, K, V, causal=True, q_rows=q_rows)  # first query sees only key 0
     assert np.array_equal(O[:, 0], V[:, 0])
+    O = mtk.attention(dev, Q, K, V, causal=True, q_rows=q_rows)  # query 256 (second block of 256)
+    assert np.array_equal(O, mtk.attention(dev, Q, K, V, causal=True, q_rows=384 - q_rows))  # both kernels: same bits
 
 
 def test_config5_full_size_sampled_rows(dev):
