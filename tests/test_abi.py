@@ -233,8 +233,8 @@ def test_attention_select_and_validation():
     # config 5: 128 query rows per workgroup by default, 256 (64 per wavefront) on request
     p = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128, causal=True)
     assert p.describe().endswith("kernels: mtk_attn_fwd_f16_causal") and "rows/wg=128 grid=2048" in p.describe()
-    p = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128, q_rows=256)
-    assert p.describe().endswith("kernels: mtk_attn_fwd_w_f16") and "rows/wg=256 grid=1024" in p.describe()
+    p256 = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128, q_rows=256)
+    assert p256.describe().endswith("kernels: mtk_attn_fwd_w_f16") and "rows/wg=256 grid=1024" in p256.describe()
     assert mtk.AttentionPlan(None, 1, 4, 1000, 1000, 128, dtype="bf16").describe().endswith("kernels: mtk_attn_fwd_bf16")
     with pytest.raises(mtk.MtkError) as e:
         mtk.AttentionPlan(None, 1, 1, 16, 16, 128, q_rows=64)
