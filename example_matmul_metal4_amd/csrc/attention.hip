@@ -81,50 +81,68 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
   // ---- direct-to-LDS staging: each wave fills 4 KB of a tile (4 rows of 256 B per instruction).
   // K: LDS chunk pc of row r holds global chunk pc ^ (r & 15); V: pc ^ 4 * (r & 3).
   int srow[4];
-  uint32_t kcol[4], vcol[4];
+  uint32_t kcol[4], vcol[4], klane[4], vlane[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     srow[i] = (wave * 4 + i) * 4 + (lane >> 4);
     const int pc = lane & 15;
     kcol[i] = 16u * (uint32_t)(pc ^ (srow[i] & 15));
     vcol[i] = 16u * (uint32_t)(pc ^ (4 * (srow[i] & 3)));
+    klane[i] = (uint32_t)srow[i] * rs + kcol[i];
+    vlane[i] = (uint32_t)srow[i] * rs + vcol[i];
   }
-  auto issue_k = [&](int slot, int t) {
-    char *dst = smem + slot * kTile + wave * 4096;
+  // A tile inside S_kv goes out with its base as the uniform scalar offset (no per-row work); the
+  // tile crossing S_kv is loaded row-checked, rows past S_kv reading zero.
+  auto issue = [&](const rsrc_t &r, char *dst, const uint32_t (&lane_off)[4], const uint32_t (&col)[4], int t) {
+    const int key0 = t * kBKV;
+    if (key0 + kBKV <= a.S_kv) {
+      const uint32_t tb = kvbase + (uint32_t)key0 * rs;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = t * kBKV + srow[i];
-      lds_direct16(rk, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + kcol[i] : kOOB);
+      for (int i = 0; i < 4; ++i) lds_direct16_s(r, dst + i * 1024, lane_off[i], tb);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = key0 + srow[i];
+        lds_direct16(r, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + col[i] : kOOB);
+      }
     }
   };
-  auto issue_v = [&](int slot, int t) {
-    char *dst = smem + (2 + slot) * kTile + wave * 4096;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = t * kBKV + srow[i];
-      lds_direct16(rv, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + vcol[i] : kOOB);
-    }
-  };
+  auto issue_k = [&](int slot, int t) { issue(rk, smem + slot * kTile + wave * 4096, klane, kcol, t); };
+  auto issue_v = [&](int slot, int t) { issue(rv, smem + (2 + slot) * kTile + wave * 4096, vlane, vcol, t); };
 
   // ---- fragment reads
+  // Fragment reads. Per-lane LDS offsets are computed once; per tile only the slot base is added
+  // (K: one offset per k-step, key block 1 at +8192; V^T: one per d block, key step js and half e
+  // at +4096 js + 1024 e, folded into the instructions' offset fields).
   const int krow = swap_bits_2_3(col);
-  auto kfrag = [&](const char *kt, int blk, int ds) -> u32x4 {
-    return *(const u32x4 *)(kt + k_off(krow + 32 * blk, 2 * ds + g));
-  };
-  // V^T fragment for d block db, key step js (16 keys): lane (h = lane / 16, s = lane % 16) gets
-  // d = 32 db + lane % 32 at keys 16 js + 8 (lane / 32) + 0..7.
-  const int vs = lane & 15, vh = lane >> 4;
-  auto vfrag = [&](const char *vt, int db, int js) -> u32x4 {
-    const int d = 32 * db + 16 * (vh & 1) + 4 * (vs & 3);
-    u32x4 v;
+  uint32_t kq[8];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int row = 16 * js + 8 * (vh >> 1) + 4 * e + (vs >> 2);
-      const u32x2 w = ds_read_tr16(vt + row * 256 + 16 * ((d >> 3) ^ (4 * (row & 3))) + 2 * (d & 7));
-      v[2 * e] = w.x;
-      v[2 * e + 1] = w.y;
-    }
-    return v;
+  for (int ds = 0; ds < 8; ++ds) kq[ds] = k_off(krow, 2 * ds + g);
+  // V^T fragment for d block db, key step js (16 keys): lane (h = lane / 16, s = lane % 16) gets
+  // d = 32 db + lane % 32 at keys 16 js + 8 (lane / 32) + 0..7 (two transposed reads, rows
+  // 16 js + 8 (h / 2) + 4 e + s / 4); the row swizzle depends only on s / 4.
+  const int vs = lane & 15, vh = lane >> 4;
+  uint32_t vq[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+    const int d = 32 * db + 16 * (vh & 1) + 4 * (vs & 3);
+    const int row = 8 * (vh >> 1) + (vs >> 2);
+    vq[db] = lds_addr(smem) + (uint32_t)(row * 256 + 16 * ((d >> 3) ^ (4 * (row & 3))) + 2 * (d & 7));
+  }
+  auto kfrag = [&](const uint32_t (&kb)[8], int blk, int ds) -> u32x4 {
+    return *(const u32x4 *)(smem + kb[ds] + blk * 8192);
+  };
+  auto kbase = [&](uint32_t (&kb)[8], int slot) {
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) kb[ds] = kq[ds] + (uint32_t)(slot * kTile);
+  };
+  auto vread = [&](u32x4 (&dst)[4], uint32_t vb) {
+    static_for<0, 4>([&](auto jc) {
+      constexpr int JS = decltype(jc)::value;
+      const u32x2 w0 = ds_read_tr16_at<4096 * JS>(vb);
+      const u32x2 w1 = ds_read_tr16_at<4096 * JS + 1024>(vb);
+      dst[JS] = u32x4{w0.x, w0.y, w1.x, w1.y};
+    });
   };
 
   float m_off = -INFINITY;  // exponent offset of this lane's query (log2 domain)
@@ -143,17 +161,18 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
     if (n_tiles > 1) issue_k(1, 1);
     issue_v(0, 0);
     {
-      const char *kt = smem;
+      uint32_t kb[8];
+      kbase(kb, 0);
 #pragma unroll
       for (int ds = 0; ds < 8; ++ds) {
-        s0 = mfma32x32x16<DT>(kfrag(kt, 0, ds), qf[ds], s0);
-        s1 = mfma32x32x16<DT>(kfrag(kt, 1, ds), qf[ds], s1);
+        s0 = mfma32x32x16<DT>(kfrag(kb, 0, ds), qf[ds], s0);
+        s1 = mfma32x32x16<DT>(kfrag(kb, 1, ds), qf[ds], s1);
       }
     }
     // row max of tile 0
-    float mx = fmaxf(s0[0], s1[0]);
+    float mx = -INFINITY;
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+    for (int r = 0; r < 16; ++r) mx = vmax3(mx, s0[r], s1[r]);
 
     for (int t = 0; t < n_tiles; ++t) {
       wait_vmem();
@@ -161,8 +180,9 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
       // (on the last tile, S(t+1) is computed from whatever the K slot holds and discarded)
       if (t + 2 < n_tiles) issue_k(t & 1, t + 2);
       if (t + 1 < n_tiles) issue_v((t + 1) & 1, t + 1);
-      const char *kn = smem + ((t + 1) & 1) * kTile;
-      const char *vt = smem + (2 + (t & 1)) * kTile;
+      uint32_t kn[8];
+      kbase(kn, (t + 1) & 1);
+      const uint32_t vt = (uint32_t)((2 + (t & 1)) * kTile);
 
       // mask of tile t (only tiles crossing S_kv or the causal diagonal)
       const int j0 = t * kBKV;
@@ -174,9 +194,9 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
           s0[r] = (key0 < a.S_kv && (!CAUSAL || key0 <= qi + diag)) ? s0[r] : -INFINITY;
           s1[r] = (key1 < a.S_kv && (!CAUSAL || key1 <= qi + diag)) ? s1[r] : -INFINITY;
         }
-        mx = fmaxf(s0[0], s1[0]);
+        mx = -INFINITY;
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+        for (int r = 0; r < 16; ++r) mx = vmax3(mx, s0[r], s1[r]);
       }
       mx = half_max(mx);
       const float m_tile = mx * c;
@@ -228,21 +248,17 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
       // phase B: O^T += V^T(t) . P^T(t), interleaved with the row max of S(t+1); the next d
       // block's V^T fragments are read while the current block's MFMAs run
       u32x4 vf[2][4];
-#pragma unroll
-      for (int js = 0; js < 4; ++js) vf[0][js] = vfrag(vt, 0, js);
-      float mn = fmaxf(n0[0], n1[0]);
+      vread(vf[0], vq[0] + vt);
+      float mn = -INFINITY;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         const int cb = db & 1, nb = cb ^ 1;
         lgkm_wait0(vf[cb]);
-        if (db + 1 < 4) {
-#pragma unroll
-          for (int js = 0; js < 4; ++js) vf[nb][js] = vfrag(vt, db + 1, js);
-        }
+        if (db + 1 < 4) vread(vf[nb], vq[db + 1] + vt);
 #pragma unroll
         for (int js = 0; js < 4; ++js) o[db] = mfma32x32x16<DT>(vf[cb][js], pf[js], o[db]);
 #pragma unroll
-        for (int r = 4 * db; r < 4 * db + 4; ++r) mn = fmaxf(mn, fmaxf(n0[r], n1[r]));
+        for (int r = 4 * db; r < 4 * db + 4; ++r) mn = vmax3(mn, n0[r], n1[r]);
         __builtin_amdgcn_sched_barrier(0);
       }
       s0 = n0;
@@ -316,47 +332,67 @@ __device__ __forceinline__ void attn_fwd_wide(const mtk_attn_kargs &a) {
   const int n_tiles = kv_end > 0 ? (kv_end + kBKV - 1) / kBKV : 0;
 
   int srow[4];
-  uint32_t kcol[4], vcol[4];
+  uint32_t kcol[4], vcol[4], klane[4], vlane[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     srow[i] = (wave * 4 + i) * 4 + (lane >> 4);
     const int pc = lane & 15;
     kcol[i] = 16u * (uint32_t)(pc ^ (srow[i] & 15));
     vcol[i] = 16u * (uint32_t)(pc ^ (4 * (srow[i] & 3)));
+    klane[i] = (uint32_t)srow[i] * rs + kcol[i];
+    vlane[i] = (uint32_t)srow[i] * rs + vcol[i];
   }
-  auto issue_k = [&](int slot, int t) {
-    char *dst = smem + slot * kTile + wave * 4096;
+  // A tile inside S_kv goes out with its base as the uniform scalar offset (no per-row work); the
+  // tile crossing S_kv is loaded row-checked, rows past S_kv reading zero.
+  auto issue = [&](const rsrc_t &r, char *dst, const uint32_t (&lane_off)[4], const uint32_t (&col)[4], int t) {
+    const int key0 = t * kBKV;
+    if (key0 + kBKV <= a.S_kv) {
+      const uint32_t tb = kvbase + (uint32_t)key0 * rs;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = t * kBKV + srow[i];
-      lds_direct16(rk, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + kcol[i] : kOOB);
+      for (int i = 0; i < 4; ++i) lds_direct16_s(r, dst + i * 1024, lane_off[i], tb);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = key0 + srow[i];
+        lds_direct16(r, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + col[i] : kOOB);
+      }
     }
   };
-  auto issue_v = [&](int slot, int t) {
-    char *dst = smem + (2 + slot) * kTile + wave * 4096;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = t * kBKV + srow[i];
-      lds_direct16(rv, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + vcol[i] : kOOB);
-    }
-  };
+  auto issue_k = [&](int slot, int t) { issue(rk, smem + slot * kTile + wave * 4096, klane, kcol, t); };
+  auto issue_v = [&](int slot, int t) { issue(rv, smem + (2 + slot) * kTile + wave * 4096, vlane, vcol, t); };
 
+  // Fragment reads. Per-lane LDS offsets are computed once; per tile only the slot base is added
+  // (K: one offset per k-step, key block 1 at +8192; V^T: one per d block, key step js and half e
+  // at +4096 js + 1024 e, folded into the instructions' offset fields).
   const int krow = swap_bits_2_3(col);
-  auto kfrag = [&](const char *kt, int blk, int ds) -> u32x4 {
-    return *(const u32x4 *)(kt + k_off(krow + 32 * blk, 2 * ds + g));
-  };
-  const int vs = lane & 15, vh = lane >> 4;
-  auto vfrag = [&](const char *vt, int db, int js) -> u32x4 {
-    const int d = 32 * db + 16 * (vh & 1) + 4 * (vs & 3);
-    u32x4 v;
+  uint32_t kq[8];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int row = 16 * js + 8 * (vh >> 1) + 4 * e + (vs >> 2);
-      const u32x2 w = ds_read_tr16(vt + row * 256 + 16 * ((d >> 3) ^ (4 * (row & 3))) + 2 * (d & 7));
-      v[2 * e] = w.x;
-      v[2 * e + 1] = w.y;
-    }
-    return v;
+  for (int ds = 0; ds < 8; ++ds) kq[ds] = k_off(krow, 2 * ds + g);
+  // V^T fragment for d block db, key step js (16 keys): lane (h = lane / 16, s = lane % 16) gets
+  // d = 32 db + lane % 32 at keys 16 js + 8 (lane / 32) + 0..7 (two transposed reads, rows
+  // 16 js + 8 (h / 2) + 4 e + s / 4); the row swizzle depends only on s / 4.
+  const int vs = lane & 15, vh = lane >> 4;
+  uint32_t vq[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) {
+    const int d = 32 * db + 16 * (vh & 1) + 4 * (vs & 3);
+    const int row = 8 * (vh >> 1) + (vs >> 2);
+    vq[db] = lds_addr(smem) + (uint32_t)(row * 256 + 16 * ((d >> 3) ^ (4 * (row & 3))) + 2 * (d & 7));
+  }
+  auto kfrag = [&](const uint32_t (&kb)[8], int blk, int ds) -> u32x4 {
+    return *(const u32x4 *)(smem + kb[ds] + blk * 8192);
+  };
+  auto kbase = [&](uint32_t (&kb)[8], int slot) {
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) kb[ds] = kq[ds] + (uint32_t)(slot * kTile);
+  };
+  auto vread = [&](u32x4 (&dst)[4], uint32_t vb) {
+    static_for<0, 4>([&](auto jc) {
+      constexpr int JS = decltype(jc)::value;
+      const u32x2 w0 = ds_read_tr16_at<4096 * JS>(vb);
+      const u32x2 w1 = ds_read_tr16_at<4096 * JS + 1024>(vb);
+      dst[JS] = u32x4{w0.x, w0.y, w1.x, w1.y};
+    });
   };
 
   float m_off[2] = {-INFINITY, -INFINITY};  // exponent offset per query block (log2 domain)
@@ -380,20 +416,22 @@ __device__ __forceinline__ void attn_fwd_wide(const mtk_attn_kargs &a) {
     __syncthreads();
     if (n_tiles > 1) issue_k(1, 1);
     issue_v(0, 0);
+    uint32_t kb0[8];
+    kbase(kb0, 0);
 #pragma unroll
     for (int ds = 0; ds < 8; ++ds)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 kf = kfrag(smem, kb, ds);
+        const u32x4 kf = kfrag(kb0, kb, ds);
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) s[kb][qb] = mfma32x32x16<DT>(kf, qf[qb][ds], s[kb][qb]);
       }
     float mx[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      mx[qb] = fmaxf(s[0][qb][0], s[1][qb][0]);
+      mx[qb] = -INFINITY;
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mx[qb] = fmaxf(mx[qb], fmaxf(s[0][qb][r], s[1][qb][r]));
+      for (int r = 0; r < 16; ++r) mx[qb] = vmax3(mx[qb], s[0][qb][r], s[1][qb][r]);
     }
 
     for (int t = 0; t < n_tiles; ++t) {
@@ -401,8 +439,9 @@ __device__ __forceinline__ void attn_fwd_wide(const mtk_attn_kargs &a) {
       __syncthreads();  // K(t+1) and V(t) are in LDS; K slot t&1 and V slot (t+1)&1 are free
       if (t + 2 < n_tiles) issue_k(t & 1, t + 2);
       if (t + 1 < n_tiles) issue_v((t + 1) & 1, t + 1);
-      const char *kn = smem + ((t + 1) & 1) * kTile;
-      const char *vt = smem + (2 + (t & 1)) * kTile;
+      uint32_t kn[8];
+      kbase(kn, (t + 1) & 1);
+      const uint32_t vt = (uint32_t)((2 + (t & 1)) * kTile);
       // K(t+1) fragments of the first two k-steps: read now, consumed after the softmax
       // bookkeeping below; later k-steps are read two k-steps ahead inside phase A
       u32x4 kf[8][2];
@@ -422,9 +461,9 @@ __device__ __forceinline__ void attn_fwd_wide(const mtk_attn_kargs &a) {
             s[0][qb][r] = (key0 < a.S_kv && (!CAUSAL || key0 <= qi[qb] + diag)) ? s[0][qb][r] : -INFINITY;
             s[1][qb][r] = (key1 < a.S_kv && (!CAUSAL || key1 <= qi[qb] + diag)) ? s[1][qb][r] : -INFINITY;
           }
-          mx[qb] = fmaxf(s[0][qb][0], s[1][qb][0]);
+          mx[qb] = -INFINITY;
 #pragma unroll
-          for (int r = 1; r < 16; ++r) mx[qb] = fmaxf(mx[qb], fmaxf(s[0][qb][r], s[1][qb][r]));
+          for (int r = 0; r < 16; ++r) mx[qb] = vmax3(mx[qb], s[0][qb][r], s[1][qb][r]);
         }
       }
       float moff[2];
@@ -460,10 +499,9 @@ __device__ __forceinline__ void attn_fwd_wide(const mtk_attn_kargs &a) {
         if (ds + 2 < 8) {
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb) kf[ds + 2][kb] = kfrag(kn, kb, ds + 2);
-        } else {
+        } else if (ds == 7) {
           // the first d block's V^T fragments for phase B (V(t) is in LDS since the barrier)
-#pragma unroll
-          for (int js = 2 * (ds - 6); js < 2 * (ds - 6) + 2; ++js) vf[0][js] = vfrag(vt, 0, js);
+          vread(vf[0], vq[0] + vt);
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -487,15 +525,12 @@ __device__ __forceinline__ void attn_fwd_wide(const mtk_attn_kargs &a) {
 
       // phase B: O^T += V^T(t) . P^T(t) for both query blocks, interleaved with the row maxima of
       // S(t+1); the next d block's V^T fragments are read while the current block's MFMAs run
-      float mn[2] = {fmaxf(n[0][0][0], n[1][0][0]), fmaxf(n[0][1][0], n[1][1][0])};
+      float mn[2] = {-INFINITY, -INFINITY};
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         const int cb = db & 1, nb = cb ^ 1;
         lgkm_wait0(vf[cb]);
-        if (db + 1 < 4) {
-#pragma unroll
-          for (int js = 0; js < 4; ++js) vf[nb][js] = vfrag(vt, db + 1, js);
-        }
+        if (db + 1 < 4) vread(vf[nb], vq[db + 1] + vt);
 #pragma unroll
         for (int js = 0; js < 4; ++js)
 #pragma unroll
@@ -503,7 +538,7 @@ __device__ __forceinline__ void attn_fwd_wide(const mtk_attn_kargs &a) {
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-          for (int r = 4 * db; r < 4 * db + 4; ++r) mn[qb] = fmaxf(mn[qb], fmaxf(n[0][qb][r], n[1][qb][r]));
+          for (int r = 4 * db; r < 4 * db + 4; ++r) mn[qb] = vmax3(mn[qb], n[0][qb][r], n[1][qb][r]);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "kargs.h"
 
 // Every code object records the kernel-argument contract it was built against; the runtime
@@ -99,7 +101,23 @@ __device__ __forceinline__ float from_bits(uint32_t h) {
 
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return (uint32_t)to_bits<DT>(lo) | ((uint32_t)to_bits<DT>(hi) << 16);
+  // written as one vector conversion: gfx950's v_cvt_pk_{f16,bf16}_f32 (round to nearest even,
+  // as to_bits) converts the pair in one instruction
+  if constexpr (DT == DT_F16) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, h2{(_Float16)lo, (_Float16)hi});
+  } else {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, b2{(__bf16)lo, (__bf16)hi});
+  }
+}
+
+// max(a, b, c) in one gfx950 v_maximum3_f32 (IEEE maximum: a NaN operand gives NaN). fmaxf on
+// values the compiler cannot prove canonical (MFMA results) is lowered with a quieting
+// v_max_f32 x, x per operand before v_max3_f32. A compiler-visible operation, not inline asm: the
+// compiler must see the read of MFMA results to insert the wait states it needs.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
 // v_perm_b32 byte selectors: low 16 bits of x, y -> (x.lo | y.lo << 16); high halves likewise.
@@ -132,6 +150,30 @@ __device__ __forceinline__ u32x2 ds_read_tr16(const char *p) {
   u32x2 w;
   asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(lds_addr(p)));
   return w;
+}
+
+// The same read at LDS byte address addr + OFF (OFF folded into the instruction's offset field).
+template <int OFF>
+__device__ __forceinline__ u32x2 ds_read_tr16_at(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  u32x2 w;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(w) : "v"(addr), "i"(OFF));
+  return w;
+}
+
+// Direct-to-LDS load with a uniform scalar offset added to the per-lane offset. The buffer range
+// check does not cover the scalar part: only for ranges known to lie inside the buffer.
+__device__ __forceinline__ void lds_direct16_s(rsrc_t r, char *lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, voff, soff, 0, 0);
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = B .. E-1.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 // Wait for every outstanding LDS read and hand registers filled by inline-asm reads on to their

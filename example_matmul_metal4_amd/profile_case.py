@@ -25,6 +25,7 @@ def main(argv=None):
     ap.add_argument("--tile", type=int, default=0)
     ap.add_argument("--mode", choices=["auto", "two_pass", "serial"], default="auto",
                     help="split-K schedule of the gemm case")
+    ap.add_argument("--rows", type=int, default=0, help="query rows per workgroup of the attention cases")
     a = ap.parse_args(argv)
 
     if a.case == "copy":
@@ -82,7 +83,7 @@ def main(argv=None):
                               dev.upload(inputs.uniform(9, (desc.O,), -1, 1)),
                               dev.empty(int(np.prod(plan.out_shape())) * 2))]
         else:
-            plan = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, causal=a.case == "attn_causal")
+            plan = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, causal=a.case == "attn_causal", q_rows=a.rows)
             shp = (2, 4096, 32, 128)
             sets = [plan.args(dev.upload(inputs.normal(10, shp)), dev.upload(inputs.normal(11, shp)),
                               dev.upload(inputs.normal(12, shp)), dev.empty(int(np.prod(shp)) * 2))]
