@@ -28,6 +28,11 @@
 //   * Global reads are raw buffer loads: keys past S_kv and queries past S_q read zero.
 //   * Causal: a workgroup stops at its last visible key tile; heavy query blocks are dispatched
 //     first; query blocks of one (batch, head) are kept on one XCD for K/V reuse in L2.
+//   * Two kernels share this arithmetic (their outputs are equal bit for bit): attn_fwd, 4
+//     wavefronts x 32 queries with the MFMA and softmax work of consecutive tiles interleaved in
+//     each wavefront, two workgroups per CU; and attn_fwd_pp, 8 wavefronts x 32 queries in two
+//     groups that alternate whole MFMA blocks and softmax blocks one block apart, so the matrix
+//     cores of a SIMD serve one group while its VALU serves the other.
 #include "device.hpp"
 
 namespace mtk {
@@ -233,15 +238,6 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
         pf[r >> 3][(r & 7) >> 1] = pack2<DT>(p00, p01);
         pf[2 + (r >> 3)][(r & 7) >> 1] = pack2<DT>(p10, p11);
       }
-      // machine-scheduler pattern for phase A: each MFMA followed by one K fragment read and a
-      // share of the softmax VALU work
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // first two K fragment reads
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        if (i < 14) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // next K fragment read
-        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
-      }
       __builtin_amdgcn_sched_barrier(0);
       l_run += psum;
 
@@ -286,27 +282,33 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Wide-query variant: 64 queries per wavefront (two 32-query blocks), 256 per workgroup, one
-// wavefront per SIMD with the whole register file. Every K fragment read from LDS feeds the S MFMAs
-// of both query blocks and every V^T fragment the P.V MFMAs of both: half the LDS reads per MFMA of
-// the 32-query kernel above, and registers to read fragments further ahead. Same data layout,
-// permutations, lazy rescale and pipeline; the softmax state is kept per query block.
-constexpr int kBQW = 256;
+// Ping-pong variant: 8 wavefronts (two per SIMD) per workgroup, 256 queries, 32 per wavefront, one
+// workgroup per CU; the K/V tiles in LDS serve all 256 queries. Each wavefront alternates an MFMA
+// block (P(t-1).V(t-1) and S(t) = K(t).Q^T: 32 MFMAs and their fragment reads, no VALU) with a VALU
+// block (mask, row max, lazy rescale, exponentials, sums, packing of tile t). The two groups of four
+// wavefronts (queries 0-127 and 128-255 of the block) run one block apart, separated by workgroup
+// barriers, so on every SIMD one wavefront is in its MFMA block while the other is in its VALU
+// block. Slot i of the schedule (between barriers i-1 and i) is, for group g and j = i - g: MFMA
+// block j/2 for even j, VALU block (j-1)/2 for odd j, nothing for j < 0 or VALU block n_tiles.
+// K(k+2) and V(k+1) are loaded during slots 2k+2 and 2k+3 (their LDS slots were last read in slot
+// 2k+1) and waited for before barrier 2k+3. Same arithmetic as the kernels above.
+constexpr int kBQP = 256;
 
 template <int DT, bool CAUSAL>
-__device__ __forceinline__ void attn_fwd_wide(const mtk_attn_kargs &a) {
+__device__ __forceinline__ void attn_fwd_pp(const mtk_attn_kargs &a) {
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTile];  // K slots 0, 1 then V slots 0, 1
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..7
+  const int grp = wave >> 2;                                  // 0: queries 0-127, 1: 128-255
   const int g = lane >> 5, col = lane & 31;
 
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = id / a.q_blocks;
-  int qb_id = id - bh * a.q_blocks;
-  if (CAUSAL) qb_id = a.q_blocks - 1 - qb_id;  // heaviest query blocks first
+  int qb = id - bh * a.q_blocks;
+  if (CAUSAL) qb = a.q_blocks - 1 - qb;  // heaviest query blocks first
   const int b = bh / a.H, h = bh - b * a.H;
-  const int q0 = qb_id * kBQW;
+  const int q0 = qb * kBQP;
   const uint32_t rs = (uint32_t)a.H * kD * 2;
   const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kD * 2);
   const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H + h) * kD * 2);
@@ -315,77 +317,59 @@ __device__ __forceinline__ void attn_fwd_wide(const mtk_attn_kargs &a) {
   const rsrc_t rv = make_rsrc(a.V, a.kv_bytes);
   const int diag = a.S_kv - a.S_q;
 
-  // this lane's two queries (one per query block) as B operands of S^T = K . Q^T
-  int qi[2];
-  u32x4 qf[2][8];
+  const int wave_q_min = q0 + wave * 32;
+  const int qi = wave_q_min + col;
+  u32x4 qf[8];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    qi[qb] = q0 + wave * 64 + qb * 32 + col;
-#pragma unroll
-    for (int ds = 0; ds < 8; ++ds)
-      qf[qb][ds] =
-          buf_load16(rq, qi[qb] < a.S_q ? qbase + (uint32_t)qi[qb] * rs + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB);
-  }
+  for (int ds = 0; ds < 8; ++ds)
+    qf[ds] = buf_load16(rq, qi < a.S_q ? qbase + (uint32_t)qi * rs + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB);
 
   int kv_end = a.S_kv;
-  if (CAUSAL) kv_end = min(a.S_kv, q0 + kBQW + diag);
+  if (CAUSAL) kv_end = min(a.S_kv, q0 + kBQP + diag);
   const int n_tiles = kv_end > 0 ? (kv_end + kBKV - 1) / kBKV : 0;
 
-  int srow[4];
-  uint32_t kcol[4], vcol[4], klane[4], vlane[4];
+  // direct-to-LDS staging: each wavefront fills 2 KB of a tile (two instructions of 4 rows). K:
+  // LDS chunk pc of row r holds global chunk pc ^ (r & 15); V: pc ^ 4 * (r & 3). Only the in-range
+  // offsets are kept in registers; the row-checked path of the tile crossing S_kv recomputes them.
+  auto stage_row = [&](int i) { return (wave * 2 + i) * 4 + (lane >> 4); };
+  auto stage_col = [&](int i, bool is_k) {
+    const int r = stage_row(i), pc = lane & 15;
+    return 16u * (uint32_t)(is_k ? (pc ^ (r & 15)) : (pc ^ (4 * (r & 3))));
+  };
+  uint32_t klane[2], vlane[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    srow[i] = (wave * 4 + i) * 4 + (lane >> 4);
-    const int pc = lane & 15;
-    kcol[i] = 16u * (uint32_t)(pc ^ (srow[i] & 15));
-    vcol[i] = 16u * (uint32_t)(pc ^ (4 * (srow[i] & 3)));
-    klane[i] = (uint32_t)srow[i] * rs + kcol[i];
-    vlane[i] = (uint32_t)srow[i] * rs + vcol[i];
+  for (int i = 0; i < 2; ++i) {
+    klane[i] = (uint32_t)stage_row(i) * rs + stage_col(i, true);
+    vlane[i] = (uint32_t)stage_row(i) * rs + stage_col(i, false);
   }
-  // A tile inside S_kv goes out with its base as the uniform scalar offset (no per-row work); the
-  // tile crossing S_kv is loaded row-checked, rows past S_kv reading zero.
-  auto issue = [&](const rsrc_t &r, char *dst, const uint32_t (&lane_off)[4], const uint32_t (&col)[4], int t) {
+  auto issue = [&](const rsrc_t &r, char *dst, const uint32_t (&lane_off)[2], bool is_k, int t) {
     const int key0 = t * kBKV;
     if (key0 + kBKV <= a.S_kv) {
       const uint32_t tb = kvbase + (uint32_t)key0 * rs;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) lds_direct16_s(r, dst + i * 1024, lane_off[i], tb);
+      for (int i = 0; i < 2; ++i) lds_direct16_s(r, dst + i * 1024, lane_off[i], tb);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = key0 + srow[i];
-        lds_direct16(r, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + col[i] : kOOB);
+      for (int i = 0; i < 2; ++i) {
+        const int key = key0 + stage_row(i);
+        lds_direct16(r, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + stage_col(i, is_k) : kOOB);
       }
     }
   };
-  auto issue_k = [&](int slot, int t) { issue(rk, smem + slot * kTile + wave * 4096, klane, kcol, t); };
-  auto issue_v = [&](int slot, int t) { issue(rv, smem + (2 + slot) * kTile + wave * 4096, vlane, vcol, t); };
+  auto issue_k = [&](int t) { issue(rk, smem + (t & 1) * kTile + wave * 2048, klane, true, t); };
+  auto issue_v = [&](int t) { issue(rv, smem + (2 + (t & 1)) * kTile + wave * 2048, vlane, false, t); };
 
-  // Fragment reads. Per-lane LDS offsets are computed once; per tile only the slot base is added
-  // (K: one offset per k-step, key block 1 at +8192; V^T: one per d block, key step js and half e
-  // at +4096 js + 1024 e, folded into the instructions' offset fields).
+  // Fragment addresses from one base per lane: K k-step ds is at chunk (2 ds + g) ^ (krow & 15) =
+  // 2 (ds ^ zh) + ((g ^ krow) & 1) with zh = (krow & 15) >> 1; V^T d block db at chunk
+  // (4 db + x) ^ 4 y = 4 (db ^ y) + x (see vread for x, y). Fewer live registers than a table.
   const int krow = swap_bits_2_3(col);
-  uint32_t kq[8];
-#pragma unroll
-  for (int ds = 0; ds < 8; ++ds) kq[ds] = k_off(krow, 2 * ds + g);
-  // V^T fragment for d block db, key step js (16 keys): lane (h = lane / 16, s = lane % 16) gets
-  // d = 32 db + lane % 32 at keys 16 js + 8 (lane / 32) + 0..7 (two transposed reads, rows
-  // 16 js + 8 (h / 2) + 4 e + s / 4); the row swizzle depends only on s / 4.
+  const uint32_t kbase0 = (uint32_t)(krow * 256 + 16 * ((g ^ krow) & 1));
+  const int kzh = (krow & 15) >> 1;
+  auto kq = [&](int ds) { return kbase0 + 32u * (uint32_t)(ds ^ kzh); };
   const int vs = lane & 15, vh = lane >> 4;
-  uint32_t vq[4];
-#pragma unroll
-  for (int db = 0; db < 4; ++db) {
-    const int d = 32 * db + 16 * (vh & 1) + 4 * (vs & 3);
-    const int row = 8 * (vh >> 1) + (vs >> 2);
-    vq[db] = lds_addr(smem) + (uint32_t)(row * 256 + 16 * ((d >> 3) ^ (4 * (row & 3))) + 2 * (d & 7));
-  }
-  auto kfrag = [&](const uint32_t (&kb)[8], int blk, int ds) -> u32x4 {
-    return *(const u32x4 *)(smem + kb[ds] + blk * 8192);
-  };
-  auto kbase = [&](uint32_t (&kb)[8], int slot) {
-#pragma unroll
-    for (int ds = 0; ds < 8; ++ds) kb[ds] = kq[ds] + (uint32_t)(slot * kTile);
-  };
+  const int vrow = 8 * (vh >> 1) + (vs >> 2), vy = vrow & 3;
+  const uint32_t vbase0 = lds_addr(smem) + (uint32_t)(vrow * 256 + 16 * (2 * (vh & 1) + ((vs & 3) >> 1)) + 2 * (4 * (vs & 3) & 7));
+  auto vq = [&](int db) { return vbase0 + 64u * (uint32_t)(db ^ vy); };
   auto vread = [&](u32x4 (&dst)[4], uint32_t vb) {
     static_for<0, 4>([&](auto jc) {
       constexpr int JS = decltype(jc)::value;
@@ -395,179 +379,178 @@ __device__ __forceinline__ void attn_fwd_wide(const mtk_attn_kargs &a) {
     });
   };
 
-  float m_off[2] = {-INFINITY, -INFINITY};  // exponent offset per query block (log2 domain)
-  float l_run[2] = {0.0f, 0.0f};            // this lane's half of the running row sums
-  f32x16 o[2][4];
+  float m_off = -INFINITY, l_run = 0.0f;
+  f32x16 o[4];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
+  f32x16 s0 = f32x16{}, s1 = f32x16{};  // S^T of the latest tile
+  u32x4 pf[4];                          // P of the latest softmaxed tile
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[qb][i] = f32x16{};
+  for (int i = 0; i < 4; ++i) pf[i] = u32x4{};
   const float c = a.scale_log2;
-  const int wave_q_min = q0 + wave * 64;
+
+  // MFMA block k: O += V(k-1)^T . P(k-1)^T (PV, k >= 1) and S(k) = K(k) . Q^T (SK, k < n_tiles),
+  // as a compile-time schedule of steps: per d block db, two S steps (k-steps 2db, 2db+1: two
+  // MFMAs on the K fragments of both key blocks) then four P.V steps (key steps js: one MFMA on one
+  // V^T fragment). Every step's fragments take exactly two LDS read instructions (inline asm:
+  // ordinary LDS reads would wait for the K/V loads of later tiles in flight), issued kLook steps
+  // ahead into a ring of registers; before its MFMAs a step waits until at most 2 * (steps issued
+  // after it) reads are outstanding (LDS reads complete in order), its registers tied to the wait.
+  constexpr int kLook = 2, kRing = kLook + 2;
+  auto mfma_block = [&](int k, auto pv_c, auto sk_c) {
+    constexpr bool PV = decltype(pv_c)::value, SK = decltype(sk_c)::value;
+    constexpr int kPerDb = (SK ? 2 : 0) + (PV ? 4 : 0), kSteps = 4 * kPerDb;
+    const uint32_t vt = (uint32_t)((2 + ((k - 1) & 1)) * kTile);
+    const uint32_t kslot = lds_addr(smem) + (uint32_t)((k & 1) * kTile);
+    u32x4 ring[kRing][2];
+    auto issue_reads = [&](auto sc) {
+      constexpr int S = decltype(sc)::value, DB = S / kPerDb, W = S % kPerDb;
+      constexpr bool IS_S = SK && W < 2;
+      if constexpr (IS_S) {
+        const uint32_t ka = kslot + kq(2 * DB + W);
+        ring[S % kRing][0] = ds_read_b128_at<0>(ka);
+        ring[S % kRing][1] = ds_read_b128_at<8192>(ka);
+      } else {
+        constexpr int JS = W - (SK ? 2 : 0);
+        const uint32_t vb = vq(DB) + vt;
+        const u32x2 w0 = ds_read_tr16_at<4096 * JS>(vb);
+        const u32x2 w1 = ds_read_tr16_at<4096 * JS + 1024>(vb);
+        ring[S % kRing][0] = u32x4{w0.x, w0.y, w1.x, w1.y};
+      }
+    };
+    if constexpr (SK) {
+      s0 = f32x16{};  // S(k) accumulates in place: VALU block k-1 is done with S(k-1)
+      s1 = f32x16{};
+    }
+    static_for<0, kLook>([&](auto sc) {
+      if constexpr (decltype(sc)::value < kSteps) issue_reads(sc);
+    });
+    static_for<0, kSteps>([&](auto sc) {
+      constexpr int S = decltype(sc)::value, DB = S / kPerDb, W = S % kPerDb;
+      constexpr bool IS_S = SK && W < 2;
+      if constexpr (S + kLook < kSteps) issue_reads(std::integral_constant<int, S + kLook>{});
+      constexpr int kYounger = 2 * ((S + kLook < kSteps) ? kLook : (kSteps - 1 - S));
+      asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(ring[S % kRing][0]), "+v"(ring[S % kRing][1]) : "i"(kYounger));
+      if constexpr (IS_S) {
+        s0 = mfma32x32x16<DT>(ring[S % kRing][0], qf[2 * DB + W], s0);
+        s1 = mfma32x32x16<DT>(ring[S % kRing][1], qf[2 * DB + W], s1);
+      } else {
+        constexpr int JS = W - (SK ? 2 : 0);
+        o[DB] = mfma32x32x16<DT>(ring[S % kRing][0], pf[JS], o[DB]);
+      }
+    });
+  };
+  // VALU block k: softmax bookkeeping and P(k)
+  auto valu_block = [&](int k) {
+    const int j0 = k * kBKV;
+    if ((j0 + kBKV > a.S_kv) || (CAUSAL && j0 + kBKV - 1 > wave_q_min + diag)) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr0 = (r < 8) ? (8 * g + r) : (16 + 8 * g + (r - 8));
+        const int key0 = j0 + kr0, key1 = j0 + 32 + kr0;
+        s0[r] = (key0 < a.S_kv && (!CAUSAL || key0 <= qi + diag)) ? s0[r] : -INFINITY;
+        s1[r] = (key1 < a.S_kv && (!CAUSAL || key1 <= qi + diag)) ? s1[r] : -INFINITY;
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = vmax3(mx, s0[r], s1[r]);
+    mx = half_max(mx);
+    const float m_tile = mx * c;
+    float alpha = 1.0f;
+    if (m_tile > m_off + kRescaleSlack) {
+      alpha = __builtin_amdgcn_exp2f(m_off - m_tile);
+      m_off = m_tile;
+    }
+    const float moff = m_off == -INFINITY ? 0.0f : m_off;
+    l_run *= alpha;
+    if (__any(alpha != 1.0f)) {
+      // one accumulator block at a time: at most 16 values in flight through temporaries
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[i] *= alpha;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    float psum = 0.0f;
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) {
+      const int r = 2 * ds;
+      const float p00 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c, -moff));
+      const float p01 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r + 1], c, -moff));
+      const float p10 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], c, -moff));
+      const float p11 = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r + 1], c, -moff));
+      psum += (p00 + p01) + (p10 + p11);
+      pf[r >> 3][(r & 7) >> 1] = pack2<DT>(p00, p01);
+      pf[2 + (r >> 3)][(r & 7) >> 1] = pack2<DT>(p10, p11);
+      __builtin_amdgcn_sched_barrier(0);  // few probabilities live at a time
+    }
+    l_run += psum;
+  };
 
   if (n_tiles > 0) {
-    f32x16 s[2][2];  // [key block][query block]: S^T of the tile being softmaxed
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) s[kb][qb] = f32x16{};
-    issue_k(0, 0);
+    issue_k(0);
+    if (n_tiles > 1) issue_k(1);
+    issue_v(0);
     wait_vmem();
     __syncthreads();
-    if (n_tiles > 1) issue_k(1, 1);
-    issue_v(0, 0);
-    uint32_t kb0[8];
-    kbase(kb0, 0);
-#pragma unroll
-    for (int ds = 0; ds < 8; ++ds)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 kf = kfrag(kb0, kb, ds);
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) s[kb][qb] = mfma32x32x16<DT>(kf, qf[qb][ds], s[kb][qb]);
+    const std::true_type T{};
+    const std::false_type F{};
+    // loads of slot 2k+2: K(k+2) and V(k+1); waited for before barrier 2k+3
+    auto loads = [&](int k) {
+      if (k + 2 < n_tiles) issue_k(k + 2);
+      if (k + 1 < n_tiles) issue_v(k + 1);
+    };
+    // Both groups run 2 n_tiles + 1 barriers. Group 0: slot 2k = MFMA block k, slot 2k+1 = VALU
+    // block k. Group 1: one slot later.
+    if (grp == 0) {
+      mfma_block(0, F, T);
+      __syncthreads();  // 0
+      for (int k = 0; k + 1 < n_tiles; ++k) {
+        valu_block(k);
+        if (k >= 1) wait_vmem();
+        __syncthreads();  // 2k+1
+        loads(k);
+        mfma_block(k + 1, T, T);
+        __syncthreads();  // 2k+2
       }
-    float mx[2];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      mx[qb] = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx[qb] = vmax3(mx[qb], s[0][qb][r], s[1][qb][r]);
-    }
-
-    for (int t = 0; t < n_tiles; ++t) {
-      wait_vmem();
-      __syncthreads();  // K(t+1) and V(t) are in LDS; K slot t&1 and V slot (t+1)&1 are free
-      if (t + 2 < n_tiles) issue_k(t & 1, t + 2);
-      if (t + 1 < n_tiles) issue_v((t + 1) & 1, t + 1);
-      uint32_t kn[8];
-      kbase(kn, (t + 1) & 1);
-      const uint32_t vt = (uint32_t)((2 + (t & 1)) * kTile);
-      // K(t+1) fragments of the first two k-steps: read now, consumed after the softmax
-      // bookkeeping below; later k-steps are read two k-steps ahead inside phase A
-      u32x4 kf[8][2];
-#pragma unroll
-      for (int ds = 0; ds < 2; ++ds)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) kf[ds][kb] = kfrag(kn, kb, ds);
-
-      const int j0 = t * kBKV;
-      if ((j0 + kBKV > a.S_kv) || (CAUSAL && j0 + kBKV - 1 > wave_q_min + diag)) {
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int kr0 = (r < 8) ? (8 * g + r) : (16 + 8 * g + (r - 8));
-            const int key0 = j0 + kr0, key1 = j0 + 32 + kr0;
-            s[0][qb][r] = (key0 < a.S_kv && (!CAUSAL || key0 <= qi[qb] + diag)) ? s[0][qb][r] : -INFINITY;
-            s[1][qb][r] = (key1 < a.S_kv && (!CAUSAL || key1 <= qi[qb] + diag)) ? s[1][qb][r] : -INFINITY;
-          }
-          mx[qb] = -INFINITY;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx[qb] = vmax3(mx[qb], s[0][qb][r], s[1][qb][r]);
-        }
+      valu_block(n_tiles - 1);
+      if (n_tiles >= 2) wait_vmem();
+      __syncthreads();  // 2N-1
+      mfma_block(n_tiles, T, F);
+      __syncthreads();  // 2N
+    } else {
+      __syncthreads();  // 0
+      mfma_block(0, F, T);
+      __syncthreads();  // 1
+      for (int k = 0; k + 1 < n_tiles; ++k) {
+        loads(k);
+        valu_block(k);
+        __syncthreads();  // 2k+2
+        mfma_block(k + 1, T, T);
+        wait_vmem();
+        __syncthreads();  // 2k+3
       }
-      float moff[2];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const float m = half_max(mx[qb]);
-        const float m_tile = m * c;
-        float alpha = 1.0f;
-        if (m_tile > m_off[qb] + kRescaleSlack) {
-          alpha = __builtin_amdgcn_exp2f(m_off[qb] - m_tile);
-          m_off[qb] = m_tile;
-        }
-        moff[qb] = m_off[qb] == -INFINITY ? 0.0f : m_off[qb];
-        l_run[qb] *= alpha;
-        if (__any(alpha != 1.0f)) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[qb][i] *= alpha;
-        }
-      }
-
-      // phase A: S(t+1) MFMAs (each K fragment feeds both query blocks) interleaved with the
-      // exponentials / sums / packing of tile t
-      f32x16 n[2][2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) n[kb][qb] = f32x16{};
-      u32x4 pf[2][4];
-      float psum[2] = {0.0f, 0.0f};
-      u32x4 vf[2][4];
-#pragma unroll
-      for (int ds = 0; ds < 8; ++ds) {
-        if (ds + 2 < 8) {
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb) kf[ds + 2][kb] = kfrag(kn, kb, ds + 2);
-        } else if (ds == 7) {
-          // the first d block's V^T fragments for phase B (V(t) is in LDS since the barrier)
-          vread(vf[0], vq[0] + vt);
-        }
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) n[kb][qb] = mfma32x32x16<DT>(kf[ds][kb], qf[qb][ds], n[kb][qb]);
-        const int r = 2 * ds;
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          const float p00 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[0][qb][r], c, -moff[qb]));
-          const float p01 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[0][qb][r + 1], c, -moff[qb]));
-          const float p10 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[1][qb][r], c, -moff[qb]));
-          const float p11 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[1][qb][r + 1], c, -moff[qb]));
-          psum[qb] += (p00 + p01) + (p10 + p11);
-          pf[qb][r >> 3][(r & 7) >> 1] = pack2<DT>(p00, p01);
-          pf[qb][2 + (r >> 3)][(r & 7) >> 1] = pack2<DT>(p10, p11);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      l_run[0] += psum[0];
-      l_run[1] += psum[1];
-
-      // phase B: O^T += V^T(t) . P^T(t) for both query blocks, interleaved with the row maxima of
-      // S(t+1); the next d block's V^T fragments are read while the current block's MFMAs run
-      float mn[2] = {-INFINITY, -INFINITY};
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const int cb = db & 1, nb = cb ^ 1;
-        lgkm_wait0(vf[cb]);
-        if (db + 1 < 4) vread(vf[nb], vq[db + 1] + vt);
-#pragma unroll
-        for (int js = 0; js < 4; ++js)
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) o[qb][db] = mfma32x32x16<DT>(vf[cb][js], pf[qb][js], o[qb][db]);
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-          for (int r = 4 * db; r < 4 * db + 4; ++r) mn[qb] = vmax3(mn[qb], n[0][qb][r], n[1][qb][r]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) s[kb][qb] = n[kb][qb];
-      mx[0] = mn[0];
-      mx[1] = mn[1];
+      valu_block(n_tiles - 1);
+      __syncthreads();  // 2N
+      mfma_block(n_tiles, T, F);
     }
   }
 
-  // ---- epilogue: O[qi][h][d] = O^T[d][qi] / l, per query block
-  uint16_t *O = (uint16_t *)a.O;
+  const float l_tot = half_sum(l_run);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (qi < a.S_q) {
+    uint16_t *O = (uint16_t *)a.O;
+    const size_t obase = (((size_t)b * a.S_q + qi) * a.H + h) * kD;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const float l_tot = half_sum(l_run[qb]);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (qi[qb] < a.S_q) {
-      const size_t obase = (((size_t)b * a.S_q + qi[qb]) * a.H + h) * kD;
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int d = db * 32 + 8 * rq + 4 * g;
-          const u32x2 v{pack2<DT>(o[qb][db][4 * rq + 0] * inv, o[qb][db][4 * rq + 1] * inv),
-                        pack2<DT>(o[qb][db][4 * rq + 2] * inv, o[qb][db][4 * rq + 3] * inv)};
-          *(u32x2 *)(O + obase + d) = v;
-        }
-    }
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = db * 32 + 8 * rq + 4 * g;
+        const u32x2 v{pack2<DT>(o[db][4 * rq + 0] * inv, o[db][4 * rq + 1] * inv),
+                      pack2<DT>(o[db][4 * rq + 2] * inv, o[db][4 * rq + 3] * inv)};
+        *(u32x2 *)(O + obase + d) = v;
+      }
   }
 }
 
@@ -586,13 +569,13 @@ ATTN_KERNEL(mtk_attn_fwd_bf16, DT_BF16, false)
 ATTN_KERNEL(mtk_attn_fwd_f16_causal, DT_F16, true)
 ATTN_KERNEL(mtk_attn_fwd_bf16_causal, DT_BF16, true)
 
-#define ATTN_WIDE_KERNEL(NAME, DT, CAUSAL)                                                             \
-  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))        \
+#define ATTN_PP_KERNEL(NAME, DT, CAUSAL)                                                               \
+  extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))        \
   NAME(const mtk_attn_kargs a) {                                                                       \
-    attn_fwd_wide<DT, CAUSAL>(a);                                                                      \
+    attn_fwd_pp<DT, CAUSAL>(a);                                                                        \
   }
 
-ATTN_WIDE_KERNEL(mtk_attn_fwd_w_f16, DT_F16, false)
-ATTN_WIDE_KERNEL(mtk_attn_fwd_w_bf16, DT_BF16, false)
-ATTN_WIDE_KERNEL(mtk_attn_fwd_w_f16_causal, DT_F16, true)
-ATTN_WIDE_KERNEL(mtk_attn_fwd_w_bf16_causal, DT_BF16, true)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_f16, DT_F16, false)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_bf16, DT_BF16, false)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_f16_causal, DT_F16, true)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_bf16_causal, DT_BF16, true)

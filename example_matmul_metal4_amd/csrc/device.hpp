@@ -161,6 +161,17 @@ __device__ __forceinline__ u32x2 ds_read_tr16_at(uint32_t addr) {
   return w;
 }
 
+// ds_read_b128 as inline asm at LDS byte address addr + OFF: like the transposed reads above, for
+// code that keeps direct-to-LDS loads in flight while it reads other LDS data (the compiler would
+// otherwise make every read wait for them); the caller waits with lgkm_wait0.
+template <int OFF>
+__device__ __forceinline__ u32x4 ds_read_b128_at(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  u32x4 w;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(w) : "v"(addr), "i"(OFF));
+  return w;
+}
+
 // Direct-to-LDS load with a uniform scalar offset added to the per-lane offset. The buffer range
 // check does not cover the scalar part: only for ranges known to lie inside the buffer.
 __device__ __forceinline__ void lds_direct16_s(rsrc_t r, char *lds, uint32_t voff, uint32_t soff) {

@@ -514,13 +514,19 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   p->kind = PLAN_ATTN;
   p->attn = d;
   p->align_a = p->align_b = 16;
-  // Query rows per workgroup: 128 (two workgroups, 8 wavefronts per CU) unless asked for. The
-  // 256-row kernel (one wavefront per SIMD, half the LDS reads per MFMA) measures slower at every
-  // size tried: with one wavefront per SIMD nothing hides its stalls.
-  const int rows = d.q_rows ? d.q_rows : 128;
+  // Query rows per workgroup: 256 (the ping-pong kernel: 8 wavefronts in two groups alternating MFMA
+  // and softmax blocks, one workgroup per CU) when its grid still fills the device and the mask is
+  // not causal; 128 (4 wavefronts, two workgroups per CU) otherwise: with causal masking the larger
+  // blocks waste more on the diagonal than the ping-pong gains.
+  int rows = d.q_rows;
+  if (rows == 0) {
+    const int cus = ctx ? ctx->prop.multiProcessorCount : 256;
+    rows = (!d.causal && (long long)d.B * d.H * ((d.S_q + 255) / 256) >= cus) ? 256 : 128;
+  }
   Launch g;
-  g.name = std::string("mtk_attn_fwd_") + (rows == 256 ? "w_" : "") + (d.dtype == MTK_F16 ? "f16" : "bf16") +
+  g.name = std::string("mtk_attn_fwd_") + (rows == 256 ? "pp_" : "") + (d.dtype == MTK_F16 ? "f16" : "bf16") +
            (d.causal ? "_causal" : "");
+  if (rows == 256) g.block = 512;  // 8 wavefronts: two groups of 4 in ping-pong
   mtk_attn_kargs a{};
   a.B = d.B;
   a.H = d.H;

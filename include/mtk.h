@@ -154,8 +154,9 @@ int mtk_gemm_run(const mtk_plan *plan, const mtk_gemm_args *args);
  * Q, O: [B][S_q][H][D]; K, V: [B][S_kv][H][D] (the reference's [S][H][D] packing,
  * attention.swift:466-468, with a batch dimension). D must be 128. scale = 1/sqrt(D).
  * causal != 0 keeps keys j <= i + (S_kv - S_q) for query i (bottom-right aligned).
- * q_rows: query rows per workgroup, 0 = let the plan choose; 128 (32 per wavefront, two
- * workgroups per CU) or 256 (64 per wavefront, one workgroup per CU: half the LDS reads per MFMA). */
+ * q_rows: query rows per workgroup, 0 = let the plan choose; 128 (4 wavefronts of 32 queries, two
+ * workgroups per CU) or 256 (8 wavefronts of 32 queries in two groups that alternate MFMA and
+ * softmax blocks, one workgroup per CU). Same results bit for bit. */
 typedef struct {
   int B, H, S_q, S_kv, D;
   int causal;

@@ -45,7 +45,7 @@ def test_code_objects_hold_every_selectable_kernel():
               for t in (128, 256)]
     names += ["mtk_splitk_reduce_f16", "mtk_splitk_reduce_bf16", "mtk_fill_u16", "mtk_skinny_f16", "mtk_skinny_bf16",
               "mtk_skinny_f16_long", "mtk_skinny_bf16_long"]
-    names += [f"mtk_attn_fwd_{w}{dt}{c}" for w in ("", "w_") for dt in ("f16", "bf16") for c in ("", "_causal")]
+    names += [f"mtk_attn_fwd_{w}{dt}{c}" for w in ("", "pp_") for dt in ("f16", "bf16") for c in ("", "_causal")]
     names += [f"mtk_conv_f16_fast_{t}_d" for t in ("256x256", "256x128", "128x128")]
     names += [f"mtk_conv_f16_gen_128x128_v{v}" for v in (8, 4, 1)]
     missing = [n for n in names if n.encode() not in blobs]
@@ -230,11 +230,12 @@ def test_conv_descriptor_validation(field, value, status):
 
 
 def test_attention_select_and_validation():
-    # config 5: 128 query rows per workgroup by default, 256 (64 per wavefront) on request
+    # config 5: non-causal -> the 256-row ping-pong kernel; causal -> 128 rows per workgroup
     p = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128, causal=True)
     assert p.describe().endswith("kernels: mtk_attn_fwd_f16_causal") and "rows/wg=128 grid=2048" in p.describe()
-    p256 = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128, q_rows=256)
-    assert p256.describe().endswith("kernels: mtk_attn_fwd_w_f16") and "rows/wg=256 grid=1024" in p256.describe()
+    p256 = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128)
+    assert p256.describe().endswith("kernels: mtk_attn_fwd_pp_f16") and "rows/wg=256 grid=1024" in p256.describe()
+    assert mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128, q_rows=128).describe().endswith("kernels: mtk_attn_fwd_f16")
     assert mtk.AttentionPlan(None, 1, 4, 1000, 1000, 128, dtype="bf16").describe().endswith("kernels: mtk_attn_fwd_bf16")
     with pytest.raises(mtk.MtkError) as e:
         mtk.AttentionPlan(None, 1, 1, 16, 16, 128, q_rows=64)
