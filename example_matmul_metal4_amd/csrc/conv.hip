@@ -7,9 +7,10 @@
 
 using namespace mtk;
 
-#define DIRECT_KERNEL(NAME, BM, BN)                                                  \
-  extern "C" __global__ void __launch_bounds__(256) NAME(const mtk_tile_args a) { \
-    tile_direct<DT_F16, BM, BN, 2, 2, OpConv<BM>, OpColsT<BN>>(a);               \
+// 256x256 tiles: 8 wavefronts (2 x 4, two per SIMD); smaller tiles: 4 (2 x 2).
+#define DIRECT_KERNEL(NAME, BM, BN, WM, WN)                                                          \
+  extern "C" __global__ void __launch_bounds__(64 * WM * WN) NAME(const mtk_tile_args a) {        \
+    tile_direct<DT_F16, BM, BN, WM, WN, OpConv<BM, WM * WN>, OpColsT<BN, WM * WN>>(a);            \
   }
 
 #define TILE_KERNEL(NAME, DT, BM, BN, WM, WN, AK, BKIND, VA, VB)                    \
@@ -17,9 +18,9 @@ using namespace mtk;
     tile_gemm<DT, BM, BN, WM, WN, AK, BKIND, VA, VB>(a);                          \
   }
 
-DIRECT_KERNEL(mtk_conv_f16_fast_256x256_d, 256, 256)
-DIRECT_KERNEL(mtk_conv_f16_fast_256x128_d, 256, 128)
-DIRECT_KERNEL(mtk_conv_f16_fast_128x128_d, 128, 128)
+DIRECT_KERNEL(mtk_conv_f16_fast_256x256_d, 256, 256, 2, 4)
+DIRECT_KERNEL(mtk_conv_f16_fast_256x128_d, 256, 128, 2, 2)
+DIRECT_KERNEL(mtk_conv_f16_fast_128x128_d, 128, 128, 2, 2)
 
 TILE_KERNEL(mtk_conv_f16_gen_128x128_v8, DT_F16, 128, 128, 2, 2, A_CONV_GENERIC, B_KN, 8, 8)
 TILE_KERNEL(mtk_conv_f16_gen_128x128_v4, DT_F16, 128, 128, 2, 2, A_CONV_GENERIC, B_KN, 4, 4)

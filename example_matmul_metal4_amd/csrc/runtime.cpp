@@ -301,6 +301,7 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   snprintf(name, sizeof name, "mtk_gemm_%s_%c%c_%dx%d_%s", dt, d.trans_a ? 't' : 'n', d.trans_b ? 't' : 'n', tile, tile,
            serial ? "s" : direct ? "d" : "v1");
   g.name = name;
+  if (tile == 256 && direct) g.block = 512;  // 256x256 direct-to-LDS tiles run 8 wavefronts
   g.grid = (unsigned)(serial ? tiles : tiles * split);
   mtk_tile_args a{};
   a.M = d.M;
@@ -442,6 +443,7 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
   else
     snprintf(name, sizeof name, "mtk_conv_f16_gen_%dx%d_v%d", bm, bn, va);
   g.name = name;
+  if (fast && bm == 256 && bn == 256) g.block = 512;  // 8 wavefronts
   mtk_tile_args a{};
   a.M = (int)M;
   a.N = d.O;

@@ -37,10 +37,14 @@ namespace mtk {
 
 // ---------------------------------------------------------------- operand policies
 
+// Every policy stages its share of a K-tile with NW wavefronts: 1 KB blocks per wavefront.
+
 // Row-major operand, K contiguous: A [M][lda] or B [N][ldb]. LDS tile [ROWS][64].
-template <int ROWS>
+template <int ROWS, int NW = 4>
 struct OpRows {
-  static constexpr int kLoads = ROWS / 32;  // 1 KB blocks per wave per K-tile
+  static constexpr int kWaves = NW;
+  static constexpr bool kIsConv = false;
+  static constexpr int kLoads = ROWS / (8 * NW);  // 1 KB blocks per wave per K-tile
   static constexpr bool kNeedsTail = true;  // the last K-tile's fragments are masked at K
   static constexpr bool kAsmFrag = false;
   uint32_t off[kLoads];
@@ -84,9 +88,11 @@ struct OpRows {
 // output pixel (n, oz, oh, ow); a 64-wide K-tile is one filter tap (kd, kh, kw) and 64 channels.
 // Per tile row the lane keeps the element offset of (n, oz*SZ-PF, oh*SY-PT, ow*SX-PL, 0) plus its
 // chunk, and the in-range taps as three bit masks packed in one word (10 bits each).
-template <int ROWS>
+template <int ROWS, int NW = 4>
 struct OpConv {
-  static constexpr int kLoads = ROWS / 32;
+  static constexpr int kWaves = NW;
+  static constexpr bool kIsConv = true;
+  static constexpr int kLoads = ROWS / (8 * NW);
   static constexpr bool kNeedsTail = false;  // K = taps * C is a multiple of 64
   static constexpr bool kAsmFrag = false;
   int pb8[kLoads];
@@ -145,10 +151,12 @@ struct OpConv {
 
 // [K][ld] operand (N contiguous): GEMM B [K][N], conv weights DHWIO = [K][O]. LDS tile [64][COLS]
 // (row = k), 16-byte chunk c of row k stored at chunk c ^ 4*(k%4).
-template <int COLS>
+template <int COLS, int NW = 4>
 struct OpColsT {
+  static constexpr int kWaves = NW;
+  static constexpr bool kIsConv = false;
   static constexpr int kRowBytes = COLS * 2;
-  static constexpr int kLoads = COLS / 32;  // 64 rows x kRowBytes / 1 KB / 4 waves
+  static constexpr int kLoads = COLS / (8 * NW);  // 64 rows x kRowBytes / 1 KB / NW waves
   static constexpr bool kNeedsTail = false;  // rows k >= K are past the operand: read as zero
   // Fragment reads are inline asm: the compiler's wait insertion cannot tell the transposed read
   // builtin apart from the in-flight direct-to-LDS writes of the other stage and would wait for
@@ -201,7 +209,9 @@ struct OpColsT {
 // same K-tiles, partition sums are added in partition order, the bias last.
 template <int DT, int BM, int BN, int WAVES_M, int WAVES_N, typename AOP, typename BOP, bool SERIAL = false>
 __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
-  static_assert(WAVES_M * WAVES_N == 4, "4 wavefronts per workgroup");
+  constexpr int NW = WAVES_M * WAVES_N;
+  static_assert(NW == 4 || NW == 8, "4 or 8 wavefronts per workgroup");
+  static_assert(AOP::kWaves == NW && BOP::kWaves == NW, "operand policies staged by the same wavefronts");
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   static_assert(TM >= TN, "fragment reads are paired per row block");
@@ -247,7 +257,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
 
   // one K-tile's loads into stage base `st`
   auto issue_all = [&](char *st, int kt) {
-    if constexpr (std::is_same<AOP, OpConv<BM>>::value) {
+    if constexpr (AOP::kIsConv) {
       const auto tp = opa.tap(a, kt);
 #pragma unroll
       for (int q = 0; q < PA; ++q) opa.issue(ra, st, q, tp);
@@ -308,8 +318,8 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       const int kn = min(kt + 1, kt1 - 1);
       const char *sa = smem + cur * kStage;
       const char *sb = sa + BM * 128;
-      typename std::conditional<std::is_same<AOP, OpConv<BM>>::value, typename OpConv<BM>::Tap, int>::type tp{};
-      if constexpr (std::is_same<AOP, OpConv<BM>>::value) tp = opa.tap(a, kn);
+      typename std::conditional<AOP::kIsConv, typename OpConv<BM, NW>::Tap, int>::type tp{};
+      if constexpr (AOP::kIsConv) tp = opa.tap(a, kn);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int ks = 0; ks < kBK / 16; ++ks) {
@@ -335,7 +345,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
           for (int u = 0; u < kPerGroup; ++u) {
             const int q = (ks * TM + i) * kPerGroup + u;
             if (q < PA) {
-              if constexpr (std::is_same<AOP, OpConv<BM>>::value)
+              if constexpr (AOP::kIsConv)
                 opa.issue(ra, nxt, q, tp);
               else
                 opa.issue(ra, nxt, q, kn);
@@ -436,7 +446,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     hi = odd ? x1 : recv;
   };
   // Split-K partials: GEMM only (convolution plans never split K).
-  constexpr bool kPartials = !SERIAL && !std::is_same<AOP, OpConv<BM>>::value;
+  constexpr bool kPartials = !SERIAL && !AOP::kIsConv;
   if (kPartials && a.partial != nullptr) {
     float *P = a.partial + (size_t)split * a.M * a.N;
     const bool vec = (a.N & 1) == 0;
@@ -469,7 +479,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     constexpr int kRowB = WTN * 2;       // bytes per sub-tile row
     constexpr int kChunks = kRowB / 16;  // 16-byte chunks per row
     static_assert(kChunks == 16 || kChunks == 8, "sub-tile width");
-    static_assert(4 * WTM * kRowB <= 2 * kStage, "C tile fits the LDS stages");
+    static_assert(NW * WTM * kRowB <= 2 * kStage, "C tile fits the LDS stages");
     // chunk swizzle: the four rows one paired write instruction touches land on disjoint banks
     auto swz = [](int rr) { return kChunks == 16 ? 4 * ((rr & 1) | ((rr >> 1) & 2)) : 4 * ((rr >> 2) & 1); };
     __syncthreads();  // every wave is done reading the last K-tile's fragments
