@@ -9,7 +9,7 @@
 
 #include <stdint.h>
 
-#define MTK_KARGS_VERSION 3
+#define MTK_KARGS_VERSION 4
 
 /* Tile-GEMM kernels: plain GEMM (A [M][K] . B, B either [N][K] or [K][N]) and
  * implicit-GEMM convolution (A = im2col of an NDHWC activation, B = DHWIO
@@ -20,8 +20,8 @@ typedef struct {
   const void *bias; /* [N] or NULL */
   void *C;          /* [M][ldc] output (f16/bf16), or NULL when writing partials */
   float *partial;   /* two-pass split-K: [split_k][M][N] fp32 partials (C NULL);
-                       in-workgroup split-K (*_s kernels): [tiles][split_k-1][BM*BN] parked
-                       partition sums (C set); else NULL */
+                       in-workgroup split-K (*_s kernels): [tiles][BM*BN] running sums of
+                       the finished partitions (C set); else NULL */
   int32_t M, N, K;
   int32_t lda, ldb, ldc;
   uint32_t a_bytes, b_bytes; /* buffer-resource ranges: loads at or past these byte offsets return 0 */
@@ -30,6 +30,10 @@ typedef struct {
   int32_t k_tiles_per_split;
   int32_t split_k;
   int32_t has_bias;
+  /* Split-K partition boundaries of output tile t: s * k_tiles_per_split + (t % k_stagger) -
+     k_stagger / 2 for 0 < s < split_k (0 when k_stagger < 2). Staggering spreads the tiles'
+     partition ends over several K-tiles while every tile still walks K in the same order. */
+  int32_t k_stagger;
   /* implicit-GEMM convolution geometry (unused by plain GEMM) */
   int32_t cN, cD, cH, cW, cC;
   int32_t cKD, cKH, cKW;

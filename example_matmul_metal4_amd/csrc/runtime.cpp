@@ -17,6 +17,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -46,6 +47,7 @@ int fail(int status, const char *fmt, ...) {
   } while (0)
 
 constexpr uint64_t kMaxOperandBytes = (1ull << 31) - 256;  // buffer-resource ranges (see device.hpp)
+constexpr int kMaxKStagger = 8;  // split-K boundary offsets span at most 8 K-tiles
 
 }  // namespace
 
@@ -318,10 +320,19 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   a.k_tiles_per_split = kps;
   a.split_k = split;
   a.has_bias = d.has_bias ? 1 : 0;
+  // Staggered partition boundaries (per-tile offsets in [-S/2, S/2)): with every tile ending a
+  // partition at the same K-tile, all workgroups store their partition sums in one burst. The
+  // span keeps the first partition and the last (which may be shorter) non-empty.
+  if (split > 1) {
+    const int last = k_tiles - (split - 1) * kps;
+    int span = std::min(kMaxKStagger, std::min(2 * (kps - 1), 2 * last));
+    if (const char *e = getenv("MTK_K_STAGGER")) span = std::min(span, atoi(e));
+    a.k_stagger = span >= 2 ? span & ~1 : 0;
+  }
   set_args(g, a);
   p->launches.push_back(g);
   if (serial) {
-    p->workspace = (size_t)tiles * (split - 1) * tile * tile * sizeof(float);
+    p->workspace = (size_t)tiles * tile * tile * sizeof(float);  // one running-sum slot per tile
   } else if (split > 1) {
     p->workspace = (size_t)split * d.M * d.N * sizeof(float);
     Launch r;

@@ -203,10 +203,11 @@ struct OpColsT {
 
 // SERIAL (GEMM split-K on a tile grid that already fills the chip, at most 4 partitions): one
 // workgroup per output tile runs the K partitions one after another through one continuous
-// pipeline. At the end of each partition but the last its fp32 sum is parked in the workspace and
-// the accumulators restart from zero; the epilogue adds the parked sums and the last one, then the
-// bias. The arithmetic is the two-pass split-K's: every partition accumulates from zero over the
-// same K-tiles, partition sums are added in partition order, the bias last.
+// pipeline. At the end of each partition but the last its fp32 sum is added to the tile's running
+// sum in the workspace and the accumulators restart from zero; the epilogue adds the running sum
+// and the last partition, then the bias. The arithmetic is the two-pass split-K's: every partition
+// accumulates from zero over the same K-tiles, partition sums are added in partition order, the
+// bias last.
 template <int DT, int BM, int BN, int WAVES_M, int WAVES_N, typename AOP, typename BOP, bool SERIAL = false>
 __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   constexpr int NW = WAVES_M * WAVES_N;
@@ -242,8 +243,8 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   const int tm = first_m + (t % group) % gm;
   const int tn = (t % group) / gm;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kt0 = SERIAL ? 0 : split_first_tile(a, split);
-  const int kt1 = SERIAL ? a.k_tiles : split_first_tile(a, split + 1);
+  const int kt0 = SERIAL ? 0 : split_first_tile(a, split, t);
+  const int kt1 = SERIAL ? a.k_tiles : split_first_tile(a, split + 1, t);
   constexpr bool kAnyTail = AOP::kNeedsTail || BOP::kNeedsTail;
   const bool tail_here = kAnyTail && (a.K % kBK) != 0 && kt1 == a.k_tiles && kt0 < kt1;
   const int kfull = tail_here ? kt1 - 1 : kt1;
@@ -275,20 +276,23 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
 
-  // SERIAL: finished partition p (p < split_k-1) of this workgroup's tile is parked in slot p of
-  // the tile's run of split_k-1 slots in the workspace ([tiles][split_k-1][BM*BN] fp32), in
-  // accumulator order (wave, block (i, j), register quad, lane): each lane moves 16 bytes per
-  // instruction, one instruction covers 1 KB of contiguous memory, and only this lane reads back
-  // what it wrote.
+  // SERIAL: the running sum of the finished partitions of this workgroup's tile lives in the
+  // tile's slot of the workspace ([tiles][BM*BN] fp32), in accumulator order (wave, block (i, j),
+  // register quad, lane): each lane moves 16 bytes per instruction, one instruction covers 1 KB of
+  // contiguous memory, and only this lane reads back what it wrote. The first boundary stores
+  // partition 0; later ones add the finished partition to the slot ((p0 + p1) + p2 ...); the
+  // epilogue adds the slot in front of the last partition. Slot loads bypass L1 (device scope), so
+  // a line read at one boundary is never served stale at the next.
   constexpr uint32_t kSlotBytes = BM * BN * 4;
   constexpr int kStorePolicy = 16;  // sc1 stores: measured faster than the default policy for the parks
-  const rsrc_t rslot = make_rsrc(SERIAL ? a.partial + (size_t)t * (a.split_k - 1) * (BM * BN) : nullptr,
-                                 SERIAL ? (uint32_t)(a.split_k - 1) * kSlotBytes : 0u);
+  constexpr int kLoadPolicy = 16;   // sc1 loads: served by L2, not by a possibly stale L1 line
+  const rsrc_t rslot = make_rsrc(SERIAL ? a.partial + (size_t)t * (BM * BN) : nullptr, SERIAL ? kSlotBytes : 0u);
   const uint32_t slot_lane = (uint32_t)(wave * (TM * TN * 1024) + lane * 4) * 4u;
-  auto slot_at = [&](int p, int i, int j, int q) {
-    return slot_lane + (uint32_t)p * kSlotBytes + (uint32_t)((i * TN + j) * 4096 + q * 1024);
+  auto slot_at = [&](int i, int j, int q) { return slot_lane + (uint32_t)((i * TN + j) * 4096 + q * 1024); };
+  auto slot_load = [&](int i, int j, int q) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rslot, slot_at(i, j, q), 0, kLoadPolicy));
   };
-  int split_end = SERIAL ? split_first_tile(a, 1) : 0;  // SERIAL: first K-tile of the next partition
+  int split_end = SERIAL ? split_first_tile(a, 1, t) : 0;  // SERIAL: first K-tile of the next partition
   int parked = 0;                                           // SERIAL: partitions parked in the workspace
   if (kt0 < kt1) issue_all(smem, kt0);
   wait_vmem();
@@ -374,18 +378,40 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       // anywhere else (or at K itself) after the last partition. Only boundaries park, so every
       // slot written is one of this tile's split_k-1.
       if (kt != split_end || split_end >= a.k_tiles || parked >= a.split_k - 1) break;
+      if (parked == 0) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+          for (int j = 0; j < TN; ++j)
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            __builtin_amdgcn_raw_buffer_store_b128(
-                __builtin_bit_cast(u32x4, f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                                                acc[i][j][4 * q + 3]}),
-                rslot, slot_at(parked, i, j, q), 0, kStorePolicy);
+            for (int q = 0; q < 4; ++q)
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  __builtin_bit_cast(u32x4, f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                                  acc[i][j][4 * q + 3]}),
+                  rslot, slot_at(i, j, q), 0, kStorePolicy);
+      } else {
+        // slot += partition sum, one accumulator block at a time, the next block's loads in flight
+        f32x4 ring[2][4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ring[0][q] = slot_load(0, 0, q);
+#pragma unroll
+        for (int b = 0; b < TM * TN; ++b) {
+          const int i = b % TM, j = b / TM;
+          if (b + 1 < TM * TN) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ring[(b + 1) & 1][q] = slot_load((b + 1) % TM, (b + 1) / TM, q);
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4 v = ring[b & 1][q] +
+                            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rslot, slot_at(i, j, q), 0,
+                                                   kStorePolicy);
+          }
+        }
+      }
       ++parked;
-      split_end = split_first_tile(a, parked + 1);
+      split_end = split_first_tile(a, parked + 1, t);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -485,20 +511,15 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     __syncthreads();  // every wave is done reading the last K-tile's fragments
     char *ct = smem + wave * (WTM * kRowB);
     const uint16_t *bias = (const uint16_t *)a.bias;
-    // SERIAL: the parked partition sums (at most 3) of each accumulator block, loaded one block
-    // ahead and added in partition order in front of the last partition's: ((p0 + p1) + p2) + acc.
-    constexpr int kMaxParked = 3;
-    const int np = SERIAL ? min(parked, kMaxParked) : 0;
-    f32x4 ring[2][kMaxParked][4];
+    // SERIAL: the running sum of the earlier partitions, loaded one accumulator block ahead and
+    // added in front of the last partition's sum.
+    const bool has_slot = SERIAL && parked > 0;
+    f32x4 ring[2][4];
     auto fetch = [&](int s, int i, int j) {
+      if (has_slot) {
 #pragma unroll
-      for (int p = 0; p < kMaxParked; ++p)
-        if (p < np) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            ring[s][p][q] =
-                __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rslot, slot_at(p, i, j, q), 0, 0));
-        }
+        for (int q = 0; q < 4; ++q) ring[s][q] = slot_load(i, j, q);
+      }
     };
     if constexpr (SERIAL) fetch(0, 0, 0);
 #pragma unroll
@@ -514,13 +535,10 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
         for (int r = 0; r < 16; ++r) x[r] = acc[i][j][r];
         if constexpr (SERIAL) {
           if (b + 1 < TM * TN) fetch((b + 1) & 1, (b + 1) % TM, (b + 1) / TM);
-          if (np > 0) {
+          if (has_slot) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              f32x4 v = ring[b & 1][0][q];
-#pragma unroll
-              for (int p = 1; p < kMaxParked; ++p)
-                if (p < np) v += ring[b & 1][p][q];
+              const f32x4 v = ring[b & 1][q];
 #pragma unroll
               for (int e = 0; e < 4; ++e) x[4 * q + e] = v[e] + x[4 * q + e];
             }

@@ -253,8 +253,14 @@ struct ASel<A_CONV_GENERIC, ROWS, V> {
 
 // First K-tile of split-K partition s of a tile (s = split_k: one past the last). Every
 // partition is non-empty: the plan picks split_k = ceil(k_tiles / k_tiles_per_split).
-__device__ __forceinline__ int split_first_tile(const mtk_tile_args &a, int s) {
-  return s >= a.split_k ? a.k_tiles : s * a.k_tiles_per_split;
+// First K-tile of split-K partition s of output tile t (partition split_k ends at k_tiles).
+// Interior boundaries move by a per-tile offset in [-k_stagger/2, k_stagger/2) (the host keeps
+// every partition non-empty).
+__device__ __forceinline__ int split_first_tile(const mtk_tile_args &a, int s, int t) {
+  if (s <= 0) return 0;
+  if (s >= a.split_k) return a.k_tiles;
+  const int off = a.k_stagger > 1 ? t % a.k_stagger - a.k_stagger / 2 : 0;
+  return s * a.k_tiles_per_split + off;
 }
 
 template <int DT, int BM, int BN, int WAVES_M, int WAVES_N, int AKIND, int BKIND, int VA, int VB>
@@ -283,8 +289,8 @@ __device__ __forceinline__ void tile_gemm(const mtk_tile_args &a) {
   const int tm = first_m + (t % group) % gm;
   const int tn = (t % group) / gm;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int kt0 = split_first_tile(a, split);
-  const int kt1 = split_first_tile(a, split + 1);
+  const int kt0 = split_first_tile(a, split, t);
+  const int kt1 = split_first_tile(a, split + 1, t);
 
   const rsrc_t ra = make_rsrc(a.A, a.a_bytes);
   const rsrc_t rb = make_rsrc(a.B, a.b_bytes);
