@@ -73,7 +73,7 @@ class DeviceInfo(ctypes.Structure):
 
 class GemmDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("M", "N", "K", "lda", "ldb", "ldc", "trans_b", "dtype", "has_bias",
-                                            "split_k", "tile", "trans_a", "split_mode")]
+                                            "split_k", "tile", "trans_a", "split_mode", "k_stagger")]
 
 
 class GemmArgs(ctypes.Structure):
@@ -355,17 +355,22 @@ def _ptr(x):
 
 class GemmPlan(_Plan):
     """C[M][N] = bias + op(A) . op(B); A is [M][K] (default) or [K][M] when trans_a (the reference's
-    transpose.left); B is [N][K] when trans_b (the reference default) else [K][N]."""
+    transpose.left); B is [N][K] when trans_b (the reference default) else [K][N].
+
+    k_stagger: split-K partition layout (0 = the plan's choice, -1 = uniform, > 0 = span of the
+    per-tile boundary offsets in K-tiles); two plans with the same layout give the same result
+    bit for bit whatever their split_mode."""
 
     _args_type = GemmArgs
     _run_fn = "mtk_gemm_run"
 
     def __init__(self, device: Device | None, M, N, K, *, trans_b=True, dtype="f16", has_bias=False, split_k=1,
-                 tile=0, lda=0, ldb=0, ldc=0, trans_a=False, split_mode="auto"):
+                 tile=0, lda=0, ldb=0, ldc=0, trans_a=False, split_mode="auto", k_stagger=0):
         self.desc = GemmDesc(M=M, N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, trans_b=1 if trans_b else 0,
                              dtype=_DT[dtype], has_bias=1 if has_bias else 0, split_k=split_k, tile=tile,
                              trans_a=1 if trans_a else 0,
-                             split_mode=_SPLIT_MODES[split_mode] if isinstance(split_mode, str) else split_mode)
+                             split_mode=_SPLIT_MODES[split_mode] if isinstance(split_mode, str) else split_mode,
+                             k_stagger=k_stagger)
         h = ctypes.c_void_p()
         _check(lib().mtk_gemm_plan(device.handle if device else None, ctypes.byref(self.desc), ctypes.byref(h)))
         super().__init__(h)

@@ -47,7 +47,7 @@ int fail(int status, const char *fmt, ...) {
   } while (0)
 
 constexpr uint64_t kMaxOperandBytes = (1ull << 31) - 256;  // buffer-resource ranges (see device.hpp)
-constexpr int kMaxKStagger = 8;  // split-K boundary offsets span at most 8 K-tiles
+constexpr int kAutoKStagger = 16;  // in-workgroup split-K: boundary offsets span up to 16 K-tiles
 
 }  // namespace
 
@@ -189,6 +189,7 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   if (d.ldc < d.N) return fail(MTK_ERR_INVALID, "ldc (%d) < N (%d)", d.ldc, d.N);
   if (d.split_k < 0) return fail(MTK_ERR_INVALID, "split_k must be >= 0");
   if (d.tile != 0 && d.tile != 128 && d.tile != 256) return fail(MTK_ERR_INVALID, "tile must be 0, 128 or 256");
+  if (d.k_stagger < -1) return fail(MTK_ERR_INVALID, "k_stagger must be >= -1 (got %d)", d.k_stagger);
   if (d.split_mode < MTK_SPLIT_AUTO || d.split_mode > MTK_SPLIT_SERIAL)
     return fail(MTK_ERR_INVALID, "split_mode must be MTK_SPLIT_AUTO, MTK_SPLIT_TWO_PASS or MTK_SPLIT_SERIAL");
   // Buffer ranges end on a whole dword: raw buffer loads range-check per dword, so a last element
@@ -321,12 +322,14 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   a.split_k = split;
   a.has_bias = d.has_bias ? 1 : 0;
   // Staggered partition boundaries (per-tile offsets in [-S/2, S/2)): with every tile ending a
-  // partition at the same K-tile, all workgroups store their partition sums in one burst. The
-  // span keeps the first partition and the last (which may be shorter) non-empty.
-  if (split > 1) {
+  // partition at the same K-tile, all workgroups of the in-workgroup schedule write their running
+  // sums in one burst. The span keeps the first partition and the last (which may be shorter)
+  // non-empty. The two-pass schedule keeps uniform partitions by default: there every partition
+  // is its own workgroup and uneven ones would unbalance the grid.
+  if (split > 1 && d.k_stagger >= 0) {
     const int last = k_tiles - (split - 1) * kps;
-    int span = std::min(kMaxKStagger, std::min(2 * (kps - 1), 2 * last));
-    if (const char *e = getenv("MTK_K_STAGGER")) span = std::min(span, atoi(e));
+    int span = std::min(2 * (kps - 1), 2 * last);
+    span = std::min(span, d.k_stagger > 0 ? d.k_stagger : serial ? kAutoKStagger : 0);
     a.k_stagger = span >= 2 ? span & ~1 : 0;
   }
   set_args(g, a);
@@ -350,10 +353,11 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
     set_args(r, ra);
     p->launches.push_back(r);
   }
-  char desc[256];
-  snprintf(desc, sizeof desc, "gemm %s %s %s M=%d N=%d K=%d tile=%dx%d split_k=%d k_tiles/split=%d %s grid=%u%s",
-           dt, d.trans_a ? "A[K][M]" : "A[M][K]", d.trans_b ? "B[N][K]" : "B[K][N]", d.M, d.N, d.K, tile, tile, split, kps,
-           direct ? "direct-to-LDS" : "2-byte loads", g.grid,
+  char desc[320];
+  snprintf(desc, sizeof desc,
+           "gemm %s %s %s M=%d N=%d K=%d tile=%dx%d split_k=%d k_tiles/split=%d k_stagger=%d %s grid=%u%s", dt,
+           d.trans_a ? "A[K][M]" : "A[M][K]", d.trans_b ? "B[N][K]" : "B[K][N]", d.M, d.N, d.K, tile, tile, split, kps,
+           a.k_stagger, direct ? "direct-to-LDS" : "2-byte loads", g.grid,
            serial ? " (partitions in sequence per tile, summed in the epilogue)" : split > 1 ? " + splitk_reduce" : "");
   p->description = desc;
   int s = resolve(p);

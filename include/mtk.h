@@ -107,17 +107,22 @@ int mtk_set_stream(mtk_ctx *ctx, void *hip_stream);
  * with the bias added last (the reference's reduce_sum_2, matmul.swift:298-311, 451-474, without
  * its in-place race); 0 = let the plan choose.
  * tile: 0 = let the plan choose; else 128 or 256 (square MFMA workgroup tile).
- * split_mode (split_k > 1): how the partitions are scheduled; the arithmetic, and so the result,
- * is the same bit for bit:
+ * split_mode (split_k > 1): how the partitions are scheduled; for one partition layout the
+ * arithmetic, and so the result, is the same bit for bit:
  *   MTK_SPLIT_AUTO     in-workgroup when the tile grid fills the device and split_k <= 4,
  *                      else two-pass;
  *   MTK_SPLIT_TWO_PASS every partition its own workgroup writing fp32 partials [split_k][M][N],
  *                      then a second kernel sums them and adds the bias (the reference's
  *                      dispatch, matmul.swift:439-474);
- *   MTK_SPLIT_SERIAL   one workgroup per output tile runs the partitions in sequence, parks the
- *                      first split_k-1 partition sums in the workspace and adds them and the bias
- *                      in its epilogue: no second kernel, (split_k-1)/split_k of the partial
- *                      traffic (split_k <= 4). */
+ *   MTK_SPLIT_SERIAL   one workgroup per output tile runs the partitions in sequence, keeps the
+ *                      running sum of the finished partitions in the workspace (one fp32 tile
+ *                      per output tile) and adds it and the bias in its epilogue: no second
+ *                      kernel (split_k <= 4).
+ * k_stagger (split_k > 1): partition layout. Partition boundaries of output tile t sit at
+ * s * ceil(k_tiles / split_k) + (t % S) - S / 2 K-tiles of 64 (0 < s < split_k), S the span:
+ *   0 = the plan's choice (in-workgroup: up to 16, which spreads the tiles' partition ends over
+ *       several K-tiles; two-pass: uniform); -1 = uniform (S = 0); > 0 = that span (rounded down
+ *       to even and to the largest span that keeps every partition non-empty). */
 #define MTK_SPLIT_AUTO 0
 #define MTK_SPLIT_TWO_PASS 1
 #define MTK_SPLIT_SERIAL 2
@@ -131,6 +136,7 @@ typedef struct {
   int tile;
   int trans_a;    /* appended: earlier fields keep their offsets */
   int split_mode; /* MTK_SPLIT_*; appended */
+  int k_stagger;  /* appended */
 } mtk_gemm_desc;
 
 /* Kernel-select. Replaces createSource(...) + makeLibrary + makeFunction(name:constantValues:) +

@@ -113,16 +113,29 @@ def test_status_strings(L):
 
 
 def test_gemm_kernel_select_dry():
-    # config 2: 256 tiles fill the device, so split-K 4 runs in-workgroup (one kernel, 3 parked
-    # partition sums per tile); the two-pass schedule on request
+    # config 2: 256 tiles fill the device, so split-K 4 runs in-workgroup (one kernel, one
+    # running-sum slot per tile, partition ends staggered over 16 K-tiles); the two-pass schedule
+    # (uniform partitions) on request
     p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4)
     d = p.describe()
     assert d.endswith("kernels: mtk_gemm_f16_nt_256x256_s") and "split_k=4" in d and "grid=256 " in d
+    assert "k_stagger=16 " in d
     assert p.workspace_bytes == 256 * 256 * 256 * 4  # one running-sum slot per tile
     p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4, split_mode="two_pass")
     d = p.describe()
     assert d.endswith("kernels: mtk_gemm_f16_nt_256x256_d mtk_splitk_reduce_f16") and "grid=1024 " in d
+    assert "k_stagger=0 " in d
     assert p.workspace_bytes == 4 * 4096 * 4096 * 4
+    # explicit layouts: uniform, a given span, and the largest span that keeps every partition
+    # non-empty (65 K-tiles, 17 per partition, the last one 14: span <= 28)
+    for ks, want in ((-1, 0), (6, 6), (7, 6), (100, 28)):
+        for mode in ("serial", "two_pass"):
+            d = mtk.GemmPlan(None, 4096, 4096, 4100, split_k=4, split_mode=mode, k_stagger=ks).describe()
+            assert f"k_stagger={want} " in d, (ks, mode, d)
+    assert "k_stagger=0 " in mtk.GemmPlan(None, 4096, 4096, 4100, split_k=1, k_stagger=8).describe()
+    # 3 K-tiles over 2 partitions (2 + 1): boundaries at K-tile 1 or 2; 2 K-tiles: no room at all
+    assert "k_stagger=2 " in mtk.GemmPlan(None, 4096, 4096, 192, split_k=2, k_stagger=8).describe()
+    assert "k_stagger=0 " in mtk.GemmPlan(None, 4096, 4096, 128, split_k=2, k_stagger=8).describe()
     # a small tile grid keeps the two-pass schedule (the partitions are the parallelism)
     assert "mtk_splitk_reduce_f16" in mtk.GemmPlan(None, 512, 512, 4100, split_k=4).describe()
     p = mtk.GemmPlan(None, 512, 512, 4100, split_k=4, split_mode="serial")
@@ -167,6 +180,7 @@ def test_gemm_kernel_select_dry():
     (dict(M=4, N=4, K=8, split_k=-2), mtk.MTK_ERR_INVALID),
     (dict(M=4, N=4, K=8, tile=64), mtk.MTK_ERR_INVALID),
     (dict(M=4, N=4, K=8, split_mode=3), mtk.MTK_ERR_INVALID),
+    (dict(M=4, N=4, K=8, k_stagger=-2), mtk.MTK_ERR_INVALID),
     (dict(M=64, N=64, K=2048, split_k=8, split_mode="serial"), mtk.MTK_ERR_UNSUPPORTED),
     (dict(M=64, N=64, K=1024, lda=1025, split_k=2, split_mode="serial"), mtk.MTK_ERR_UNSUPPORTED),
     (dict(M=70000, N=4, K=20000), mtk.MTK_ERR_UNSUPPORTED),

@@ -222,32 +222,33 @@ def test_transpose_left(dev, M, N, K, trans_b, dtype, split_k, tile):
     assert oracle.compare(_f32(got, dtype), _f32(ref, dtype), rel_tol=rel_tol)["ok"]
 
 
-@pytest.mark.parametrize("M,N,K,lda,ldb,trans_a,trans_b,dtype,split_k,tile", [
-    (512, 512, 4100, 0, 0, False, True, "f16", 4, 128),     # K tail in the last partition
-    (300, 200, 1000, 0, 0, False, False, "f16", 3, 128),    # ragged tiles, B [K][N]
-    (256, 256, 4101, 4102, 4104, False, True, "f16", 4, 256),  # odd K, padded rows
-    (64, 40, 200, 0, 0, False, True, "f16", 4, 256),        # 4 K-tiles: the last partition is the partial tile
-    (1024, 1024, 2048, 0, 0, False, True, "f16", 4, 256),   # no K tail: the last partition ends at K
-    (384, 320, 1536, 0, 0, True, True, "bf16", 2, 128),     # A [K][M]
-    (384, 320, 1500, 0, 0, True, False, "bf16", 3, 256),    # A [K][M], B [K][N]
-    (4096, 4096, 4100, 0, 0, False, True, "f16", 4, 0),     # config 2 at full size
+@pytest.mark.parametrize("M,N,K,lda,ldb,trans_a,trans_b,dtype,split_k,tile,k_stagger", [
+    (512, 512, 4100, 0, 0, False, True, "f16", 4, 128, -1),     # K tail in the last partition
+    (512, 512, 4100, 0, 0, False, True, "f16", 4, 128, 16),     # staggered partition ends
+    (300, 200, 1000, 0, 0, False, False, "f16", 3, 128, 4),     # ragged tiles, B [K][N]
+    (256, 256, 4101, 4102, 4104, False, True, "f16", 4, 256, 6),  # odd K, padded rows
+    (64, 40, 200, 0, 0, False, True, "f16", 4, 256, -1),        # 4 K-tiles: the last partition is the partial tile
+    (1024, 1024, 2048, 0, 0, False, True, "f16", 4, 256, 8),    # no K tail: the last partition ends at K
+    (384, 320, 1536, 0, 0, True, True, "bf16", 2, 128, 10),     # A [K][M]
+    (384, 320, 1500, 0, 0, True, False, "bf16", 3, 256, -1),    # A [K][M], B [K][N]
+    (4096, 4096, 4100, 0, 0, False, True, "f16", 4, 0, 16),     # config 2 at full size, its default layout
 ])
-def test_split_k_schedules_identical(dev, M, N, K, lda, ldb, trans_a, trans_b, dtype, split_k, tile):
-    # In-workgroup split-K (partitions in sequence, parked sums added in the epilogue) and the
-    # two-pass schedule do the same arithmetic: the outputs agree bit for bit; the in-workgroup one
-    # also passes the oracle check.
+def test_split_k_schedules_identical(dev, M, N, K, lda, ldb, trans_a, trans_b, dtype, split_k, tile, k_stagger):
+    # In-workgroup split-K (partitions in sequence, running sum in the workspace, added in the
+    # epilogue) and the two-pass schedule do the same arithmetic for one partition layout: the
+    # outputs agree bit for bit; the in-workgroup one also passes the oracle check.
     a_shape = (K, lda or M) if trans_a else (M, lda or K)
     b_shape = (N, ldb or K) if trans_b else (K, ldb or N)
     A = oracle.normal(80, a_shape, 0, 1 / np.sqrt(K), dtype)
     B = oracle.normal(81, b_shape, 0, 1 / np.sqrt(K), dtype)
     bias = oracle.uniform(82, (N,), -0.5, 0.5, dtype)
     print(f"[gemm] split schedules M={M} N={N} K={K} lda={lda} ldb={ldb} trans_a={trans_a} trans_b={trans_b} "
-          f"{dtype} split_k={split_k} tile={tile}", flush=True)
+          f"{dtype} split_k={split_k} tile={tile} k_stagger={k_stagger}", flush=True)
     dA, dB, db = dev.upload(A), dev.upload(B), dev.upload(bias)
     outs = {}
     for mode in ("serial", "two_pass"):
         plan = mtk.GemmPlan(dev, M, N, K, trans_a=trans_a, trans_b=trans_b, dtype=dtype, has_bias=True,
-                            split_k=split_k, tile=tile, lda=lda, ldb=ldb, split_mode=mode)
+                            split_k=split_k, tile=tile, lda=lda, ldb=ldb, split_mode=mode, k_stagger=k_stagger)
         kernel = plan.describe().split()[-1]
         assert (kernel.rsplit("_", 1)[1][0] == "s") == (mode == "serial"), plan.describe()
         dC, ws = dev.empty(M * N * 2), dev.empty(plan.workspace_bytes)
