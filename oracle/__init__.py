@@ -114,6 +114,8 @@ def lib():
                                          ctypes.c_size_t]
         L.oracle_gemm.argtypes = [ctypes.c_int] * 5 + [u16p, u16p, u16p, f32p] + [ctypes.c_int] * 3
         L.oracle_attention.argtypes = [ctypes.c_int] * 7 + [u16p, u16p, u16p, f32p] + [ctypes.c_int] * 3
+        L.oracle_attention_bwd.argtypes = ([ctypes.c_int] * 7 + [u16p, u16p, u16p, u16p, f32p, f32p, f32p, f32p]
+                                           + [ctypes.c_int] * 3)
         L.oracle_conv_out_d.argtypes = [ctypes.POINTER(ConvDims)]
         L.oracle_conv.argtypes = [ctypes.POINTER(ConvDims), u16p, u16p, u16p, f32p, ctypes.c_long, ctypes.c_long,
                                   ctypes.c_int]
@@ -209,6 +211,29 @@ def attention(Q, K, V, *, causal=False, dtype="f16", rows=None, threads=0) -> np
     q0, q1 = rows if rows is not None else (0, Sq)
     lib().oracle_attention(_dt(dtype), B, H, Sq, Skv, D, 1 if causal else 0, pq, pk, pv, _f32p(O), q0, q1, threads)
     return O
+
+
+def attention_bwd(Q, K, V, dO, *, causal=False, dtype="f16", pairs=None, threads=0):
+    """fp32 (dQ, dK, dV, Dterm) of the reference's loss sum(dO * O) for Q, K, V, dO laid out
+    [B][S][H][D] (Network.swift:205-281, 313-402); Dterm is [B][H][S_q].
+
+    ``pairs=(p0, p1)`` computes only the (b, h) pairs with flat index b*H + h in [p0, p1); the
+    other slices of the outputs stay zero."""
+    q, pq = _u16(Q)
+    k, pk = _u16(K)
+    v, pv = _u16(V)
+    g, pg = _u16(dO)
+    B, Sq, H, D = q.shape
+    Skv = k.shape[1]
+    assert k.shape == (B, Skv, H, D) and v.shape == k.shape and g.shape == q.shape
+    dQ = np.zeros((B, Sq, H, D), np.float32)
+    dK = np.zeros((B, Skv, H, D), np.float32)
+    dV = np.zeros((B, Skv, H, D), np.float32)
+    Dt = np.zeros((B, H, Sq), np.float32)
+    p0, p1 = pairs if pairs is not None else (0, -1)
+    lib().oracle_attention_bwd(_dt(dtype), B, H, Sq, Skv, D, 1 if causal else 0, pq, pk, pv, pg, _f32p(dQ),
+                               _f32p(dK), _f32p(dV), _f32p(Dt), p0, p1, threads)
+    return dQ, dK, dV, Dt
 
 
 def conv(dims: ConvDims, x, w, bias=None, *, rows=None, threads=0) -> np.ndarray:

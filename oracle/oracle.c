@@ -229,6 +229,126 @@ void oracle_attention(int dtype, int B, int H, int S_q, int S_kv, int D, int cau
 
 /* ------------------------------------------------------------------ convolution */
 
+void oracle_attention_bwd(int dtype, int B, int H, int S_q, int S_kv, int D, int causal, const uint16_t *Q,
+                          const uint16_t *K, const uint16_t *V, const uint16_t *dO, float *dQ, float *dK, float *dV,
+                          float *Dterm, int bh_begin, int bh_end, int nthreads) {
+  /* Per (b, h), rows i ascending (Network.swift): P row (createMatrixPRow, 151-179), O row = P.V and
+   * D = O . dO (createDerivativeSRow 221-238), dP row = dO.V^T (205-218), dS = P (dP - D) * scale
+   * (240-251); dQ row = dS.K, columns ascending per d (derivativeQ 376-401); dV[j] += P_j dO[i] and
+   * dK[j] += dS_j Q[i], accumulated over rows in order (derivativeV 319-338, derivativeK 341-360).
+   * One thread owns one (b, h), so every sum keeps the reference's order. */
+  if (bh_begin < 0) bh_begin = 0;
+  if (bh_end < 0 || bh_end > B * H) bh_end = B * H;
+  const float scale = 1.0f / sqrtf((float)D);
+  const size_t ldq = (size_t)H * D;
+  int nt = pick_threads(nthreads);
+  if (nt > bh_end - bh_begin) nt = bh_end - bh_begin > 0 ? bh_end - bh_begin : 1;
+#pragma omp parallel num_threads(nt)
+  {
+    float *srow = (float *)malloc(sizeof(float) * (size_t)(S_kv > 0 ? S_kv : 1));
+    float *dprow = (float *)malloc(sizeof(float) * (size_t)(S_kv > 0 ? S_kv : 1));
+    float *q = (float *)malloc(sizeof(float) * (size_t)D);
+    float *go = (float *)malloc(sizeof(float) * (size_t)D);
+    float *o = (float *)malloc(sizeof(float) * (size_t)D);
+    float *dq = (float *)malloc(sizeof(float) * (size_t)D);
+    float *kf = (float *)malloc(sizeof(float) * (size_t)S_kv * D + 1);
+    float *vf = (float *)malloc(sizeof(float) * (size_t)S_kv * D + 1);
+    float *dk = (float *)malloc(sizeof(float) * (size_t)S_kv * D + 1);
+    float *dv = (float *)malloc(sizeof(float) * (size_t)S_kv * D + 1);
+#pragma omp for schedule(dynamic, 1)
+    for (int bh = bh_begin; bh < bh_end; ++bh) {
+      const int b = bh / H, h = bh % H;
+      const uint16_t *kb = K + (size_t)b * S_kv * ldq + (size_t)h * D;
+      const uint16_t *vb = V + (size_t)b * S_kv * ldq + (size_t)h * D;
+      for (int j = 0; j < S_kv; ++j)
+        for (int d = 0; d < D; ++d) {
+          kf[(size_t)j * D + d] = to_f32(dtype, kb[(size_t)j * ldq + d]);
+          vf[(size_t)j * D + d] = to_f32(dtype, vb[(size_t)j * ldq + d]);
+        }
+      memset(dk, 0, sizeof(float) * (size_t)S_kv * D);
+      memset(dv, 0, sizeof(float) * (size_t)S_kv * D);
+      for (int i = 0; i < S_q; ++i) {
+        const uint16_t *qp = Q + ((size_t)b * S_q + i) * ldq + (size_t)h * D;
+        const uint16_t *gp = dO + ((size_t)b * S_q + i) * ldq + (size_t)h * D;
+        int ncols = S_kv;
+        if (causal) {
+          long lim = (long)i + (S_kv - S_q) + 1;
+          ncols = lim < 0 ? 0 : (lim > S_kv ? S_kv : (int)lim);
+        }
+        for (int d = 0; d < D; ++d) {
+          q[d] = to_f32(dtype, qp[d]);
+          go[d] = to_f32(dtype, gp[d]);
+          o[d] = 0.0f;
+          dq[d] = 0.0f;
+        }
+        float term_d = 0.0f;
+        if (ncols > 0) {
+          for (int j = 0; j < ncols; ++j) { /* S row */
+            const float *kp = kf + (size_t)j * D;
+            float dot = 0.0f;
+            for (int d = 0; d < D; ++d) dot += q[d] * kp[d];
+            srow[j] = dot;
+          }
+          float maximum = -3.40282347e38f;
+          for (int j = 0; j < ncols; ++j) {
+            float v = scale * srow[j];
+            maximum = v > maximum ? v : maximum;
+          }
+          float sum = 0.0f;
+          for (int j = 0; j < ncols; ++j) sum += expf(scale * srow[j] - maximum);
+          const float lse = maximum + logf(sum);
+          for (int j = 0; j < ncols; ++j) srow[j] = expf(scale * srow[j] - lse); /* P row */
+          for (int j = 0; j < ncols; ++j) { /* O = P.V, j ascending per d */
+            const float *vp = vf + (size_t)j * D;
+            const float p = srow[j];
+            for (int d = 0; d < D; ++d) o[d] += p * vp[d];
+          }
+          for (int d = 0; d < D; ++d) term_d += o[d] * go[d];
+          for (int j = 0; j < ncols; ++j) { /* dP row = dO . V^T */
+            const float *vp = vf + (size_t)j * D;
+            float dot = 0.0f;
+            for (int d = 0; d < D; ++d) dot += go[d] * vp[d];
+            dprow[j] = dot;
+          }
+          for (int j = 0; j < ncols; ++j) { /* dS row; dQ, dK, dV updates */
+            float ds = srow[j] * (dprow[j] - term_d);
+            ds *= scale;
+            const float p = srow[j];
+            const float *kp = kf + (size_t)j * D;
+            float *dkp = dk + (size_t)j * D, *dvp = dv + (size_t)j * D;
+            for (int d = 0; d < D; ++d) {
+              dq[d] += ds * kp[d];
+              dvp[d] += p * go[d];
+              dkp[d] += ds * q[d];
+            }
+          }
+        }
+        if (Dterm) Dterm[((size_t)b * H + h) * S_q + i] = term_d;
+        float *dqp = dQ + ((size_t)b * S_q + i) * ldq + (size_t)h * D;
+        for (int d = 0; d < D; ++d) dqp[d] = dq[d];
+      }
+      for (int j = 0; j < S_kv; ++j) {
+        float *dkp = dK + ((size_t)b * S_kv + j) * ldq + (size_t)h * D;
+        float *dvp = dV + ((size_t)b * S_kv + j) * ldq + (size_t)h * D;
+        for (int d = 0; d < D; ++d) {
+          dkp[d] = dk[(size_t)j * D + d];
+          dvp[d] = dv[(size_t)j * D + d];
+        }
+      }
+    }
+    free(srow);
+    free(dprow);
+    free(q);
+    free(go);
+    free(o);
+    free(dq);
+    free(kf);
+    free(vf);
+    free(dk);
+    free(dv);
+  }
+}
+
 int oracle_conv_out_d(const oracle_conv_dims *d) {
   return (d->D + d->PF + d->PBk - ((d->KD - 1) * d->DZ + 1)) / d->SZ + 1;
 }

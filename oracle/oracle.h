@@ -9,6 +9,8 @@
  * Sources restated (all paths under the reference repo):
  *   GEMM      Sources/matmul/matmul.swift:498-510        (fp32, bias first, i inner)
  *   attention Sources/attention/Network.swift:134-179, 286-311
+ *   attention backward  Sources/attention/Network.swift:205-281 (dP, D-term, dS rows),
+ *             313-402 (dV = P^T dO, dK = dS^T Q, dQ = dS K)
  *   conv2d    Sources/ConvolutionShared/ConvolutionShared.swift:4994-5026
  *   conv3d    Sources/ConvolutionShared/ConvolutionShared.swift:5028-5068
  *   conv+bias Sources/ConvolutionShared/ConvolutionShared.swift:5070-5096
@@ -58,6 +60,15 @@ void oracle_gemm(int dtype, int M, int N, int K, int trans_b, const uint16_t *A,
  * causal != 0 keeps keys j <= i + (S_kv - S_q). */
 void oracle_attention(int dtype, int B, int H, int S_q, int S_kv, int D, int causal, const uint16_t *Q,
                       const uint16_t *K, const uint16_t *V, float *O, int q_begin, int q_end, int nthreads);
+
+/* ---- attention backward (gradients of the reference's loss Phi = sum dO * O), layout
+ * [B][S][H][D] for Q/K/V/dO and for the fp32 outputs dQ/dK/dV. The (b, h) pairs with flat index
+ * b*H + h in [bh_begin, bh_end) are computed (bh_end < 0: all); their slices of dQ/dK/dV are
+ * overwritten, other slices are left alone. Dterm ([B][H][S_q] fp32, the row sums
+ * dO . O with O = P.V in fp32) may be NULL. causal != 0 as in oracle_attention. */
+void oracle_attention_bwd(int dtype, int B, int H, int S_q, int S_kv, int D, int causal, const uint16_t *Q,
+                          const uint16_t *K, const uint16_t *V, const uint16_t *dO, float *dQ, float *dK, float *dV,
+                          float *Dterm, int bh_begin, int bh_end, int nthreads);
 
 /* ---- convolution (cross-correlation), NDHWC activation, DHWIO weights,
  * NDHWC output. A 2-D convolution is D = KD = 1 with no depth padding. */

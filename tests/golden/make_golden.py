@@ -11,7 +11,8 @@ Outputs
   or dense 1..9 kernel, "same" zero padding. The expected values are computed
   here by an independent pure-Python loop over a zero-padded copy of the input
   (pad first, then correlate), not by the oracle.
-* ``seeded.npz`` -- small seeded inputs (by seed) and the oracle's fp32 outputs,
+* ``seeded.npz`` -- small seeded inputs (by seed) and the oracle's fp32 outputs (GEMM,
+  attention forward, attention backward),
   a regression pin for the oracle and the first thing the GPU tests check.
 
 The seeded fixtures are regenerated bit-identically by the SplitMix64 + RNE
@@ -145,6 +146,15 @@ def main():
     fx["attn_Q"], fx["attn_K"], fx["attn_V"] = Q, K, V
     fx["attn_O"] = oracle.attention(Q, K, V)
     fx["attn_O_causal"] = oracle.attention(Q, K, V, causal=True)
+    # attention backward (gradients of sum(dO * O)), one head, ragged S, causal and not
+    Q = oracle.normal(13, (1, 21, 1, 128))
+    K = oracle.normal(14, (1, 21, 1, 128))
+    V = oracle.normal(15, (1, 21, 1, 128))
+    G = oracle.normal(16, (1, 21, 1, 128))
+    fx["bwd_Q"], fx["bwd_K"], fx["bwd_V"], fx["bwd_dO"] = Q, K, V, G
+    for tag, causal in (("", False), ("_causal", True)):
+        dQ, dK, dV, Dt = oracle.attention_bwd(Q, K, V, G, causal=causal)
+        fx["bwd_dQ" + tag], fx["bwd_dK" + tag], fx["bwd_dV" + tag], fx["bwd_D" + tag] = dQ, dK, dV, Dt
     np.savez_compressed(os.path.join(HERE, "seeded.npz"), **fx)
     print("wrote", sorted(os.listdir(HERE)))
 

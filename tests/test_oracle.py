@@ -247,6 +247,125 @@ def _case_data(generator, dims):
     return gen.conv3d_activation(dims), gen.conv3d_weights(dims)
 
 
+
+# ---------------------------------------------------------------- attention backward
+
+def _bwd_autograd_f64(Q, K, V, G, causal):
+    """float64 gradients of sum(G * O) by torch autograd (CPU): independent of the oracle's loops."""
+    import torch
+
+    t = lambda x: torch.tensor(np.asarray(x, np.float64)).permute(0, 2, 1, 3).contiguous().requires_grad_(True)
+    q, k, v = t(Q), t(K), t(V)
+    g = torch.tensor(np.asarray(G, np.float64)).permute(0, 2, 1, 3)
+    D, Sq, Skv = q.shape[-1], q.shape[2], k.shape[2]
+    s = q @ k.transpose(-1, -2).contiguous() / np.sqrt(D)
+    p_keep = torch.ones(Sq, 1, dtype=torch.float64)
+    if causal:
+        mask = torch.arange(Skv)[None, :] > (torch.arange(Sq)[:, None] + (Skv - Sq))
+        s = s.masked_fill(mask, -1e30)  # exp underflows to exactly 0
+        p_keep = (~mask.all(-1, keepdim=True)).to(torch.float64)  # rows with no visible key: O = 0
+    o = (torch.softmax(s, -1) * p_keep) @ v
+    (o * g).sum().backward()
+    back = lambda x: x.grad.permute(0, 2, 1, 3).numpy()
+    return back(q), back(k), back(v)
+
+
+@pytest.mark.parametrize("causal,Sq,Skv", [(False, 33, 33), (True, 33, 33), (False, 17, 40), (True, 40, 17)])
+def test_attention_bwd_vs_autograd(orc, causal, Sq, Skv):
+    # Network.swift:313-402 restated; checked against float64 autograd of the same loss on the
+    # same (f16-rounded) inputs, including S_q != S_kv and the bottom-right causal alignment
+    B, H, D = 2, 2, 64
+    Q = orc.normal(50, (B, Sq, H, D))
+    K = orc.normal(51, (B, Skv, H, D))
+    V = orc.normal(52, (B, Skv, H, D))
+    G = orc.normal(53, (B, Sq, H, D))
+    dQ, dK, dV, _ = orc.attention_bwd(Q, K, V, G, causal=causal)
+    for name, got, ref in zip(("dQ", "dK", "dV"), (dQ, dK, dV), _bwd_autograd_f64(Q, K, V, G, causal)):
+        err = np.abs(got - ref).max()
+        assert err <= 2e-5 * max(1.0, np.abs(ref).max()), (name, err)
+
+
+def test_attention_bwd_finite_differences(orc):
+    # The reference's own recipe (Network.swift:45-59): perturb one entry of Q, K or V by +-0.001,
+    # difference the loss Phi = sum dO * O (here in float64), divide by 0.002.
+    B, S, H, D = 1, 9, 1, 16
+    Q = orc.normal(60, (B, S, H, D))
+    K = orc.normal(61, (B, S, H, D))
+    V = orc.normal(62, (B, S, H, D))
+    G = orc.normal(63, (B, S, H, D))
+    for causal in (False, True):
+        dQ, dK, dV, _ = orc.attention_bwd(Q, K, V, G, causal=causal)
+        base = [x.astype(np.float64) for x in (Q, K, V)]
+        rng = np.random.default_rng(7)
+        for which, grad in ((0, dQ), (1, dK), (2, dV)):
+            for _ in range(6):
+                idx = (0, rng.integers(S), 0, rng.integers(D))
+                vals = []
+                for step in (+1e-3, -1e-3):
+                    xs = [x.copy() for x in base]
+                    xs[which][idx] += step
+                    O, _ = attention_f64(*xs, causal)
+                    vals.append(float(np.sum(G.astype(np.float64) * O)))
+                fd = (vals[0] - vals[1]) / 2e-3
+                assert abs(fd - grad[idx]) <= 1e-4 * max(1.0, abs(fd)), (which, idx, fd, grad[idx])
+
+
+def test_attention_bwd_closed_forms(orc):
+    B, S, H, D = 1, 23, 2, 32
+    K = orc.normal(70, (B, S, H, D))
+    Q = orc.normal(71, (B, S, H, D))
+    G = orc.normal(72, (B, S, H, D))
+    # constant V rows: O = v for every query, so dP_ij = dO_i . v = D_i and dS = 0: dQ = dK = 0
+    row = orc.normal(73, (1, 1, H, D))
+    Vc = np.broadcast_to(row, (B, S, H, D)).copy()
+    dQ, dK, dV, Dt = orc.attention_bwd(Q, K, Vc, G)
+    scale = np.abs(G.astype(np.float64)).max() * np.abs(row.astype(np.float64)).sum() * np.abs(K.astype(np.float64)).max()
+    assert np.abs(dQ).max() <= 1e-5 * scale and np.abs(dK).max() <= 1e-5 * scale
+    # Q = 0 (non-causal): uniform P = 1/S, so every dV row is the mean of the dO rows
+    V = orc.normal(74, (B, S, H, D))
+    dQ, dK, dV, Dt = orc.attention_bwd(np.zeros_like(Q), K, V, G)
+    mean = G.astype(np.float64).mean(1, keepdims=True)
+    assert np.allclose(dV, np.broadcast_to(mean, dV.shape), atol=2e-6)
+    # D-term = sum_d O . dO with O from the forward oracle, summed over d in order in fp32
+    O = orc.attention(Q, K, V)
+    _, _, _, Dt = orc.attention_bwd(Q, K, V, G)
+    acc = np.zeros((B, S, H), np.float32)
+    g32 = G.astype(np.float32)
+    for d in range(D):
+        acc = (acc + O[..., d] * g32[..., d]).astype(np.float32)
+    assert np.array_equal(Dt, acc.transpose(0, 2, 1))
+
+
+def test_attention_bwd_key_permutation_equivariance(orc):
+    # permuting keys and values together permutes dK, dV the same way and leaves dQ unchanged
+    Q = orc.normal(80, (1, 16, 1, 64))
+    K = orc.normal(81, (1, 16, 1, 64))
+    V = orc.normal(82, (1, 16, 1, 64))
+    G = orc.normal(83, (1, 16, 1, 64))
+    perm = np.random.default_rng(5).permutation(16)
+    dQ, dK, dV, _ = orc.attention_bwd(Q, K, V, G)
+    pQ, pK, pV, _ = orc.attention_bwd(Q, K[:, perm], V[:, perm], G)
+    assert np.allclose(dQ, pQ, atol=1e-5) and np.allclose(dK[:, perm], pK, atol=1e-5)
+    assert np.allclose(dV[:, perm], pV, atol=1e-5)
+    # ...and computing only some (b, h) pairs leaves the others untouched and the computed ones equal
+    Q2 = orc.normal(84, (2, 16, 3, 64))
+    K2 = orc.normal(85, (2, 16, 3, 64))
+    V2 = orc.normal(86, (2, 16, 3, 64))
+    G2 = orc.normal(87, (2, 16, 3, 64))
+    full = orc.attention_bwd(Q2, K2, V2, G2)
+    part = orc.attention_bwd(Q2, K2, V2, G2, pairs=(2, 4))  # (b, h) = (0, 2), (1, 0)
+    for f, p in zip(full[:3], part[:3]):
+        assert np.array_equal(p[0, :, 2], f[0, :, 2]) and np.array_equal(p[1, :, 0], f[1, :, 0])
+        assert not p[0, :, :2].any() and not p[1, :, 1:].any()
+
+
+def test_attention_bwd_fixture_regression(orc, golden_dir):
+    fx = np.load(os.path.join(golden_dir, "seeded.npz"))
+    for tag, causal in (("", False), ("_causal", True)):
+        dQ, dK, dV, Dt = orc.attention_bwd(fx["bwd_Q"], fx["bwd_K"], fx["bwd_V"], fx["bwd_dO"], causal=causal)
+        assert np.array_equal(dQ, fx["bwd_dQ" + tag]) and np.array_equal(dK, fx["bwd_dK" + tag])
+        assert np.array_equal(dV, fx["bwd_dV" + tag]) and np.array_equal(Dt, fx["bwd_D" + tag])
+
 def test_conv_reference_cases_exact(orc, golden_dir):
     """Every reference case list, on the reference's integer generators: oracle fp32 == float64, bit-exact."""
     cases = json.load(open(os.path.join(golden_dir, "cases.json")))
