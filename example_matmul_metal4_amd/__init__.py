@@ -86,7 +86,12 @@ class AttnDesc(ctypes.Structure):
 
 
 class AttnArgs(ctypes.Structure):
-    _fields_ = [("Q", ctypes.c_void_p), ("K", ctypes.c_void_p), ("V", ctypes.c_void_p), ("O", ctypes.c_void_p)]
+    _fields_ = [("Q", ctypes.c_void_p), ("K", ctypes.c_void_p), ("V", ctypes.c_void_p), ("O", ctypes.c_void_p),
+                ("lse", ctypes.c_void_p)]
+
+
+class AttnBwdArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("Q", "K", "V", "O", "dO", "lse", "dQ", "dK", "dV", "workspace")]
 
 
 class ConvDesc(ctypes.Structure):
@@ -136,6 +141,8 @@ SIGNATURES = {
     "mtk_gemm_run": (ctypes.c_int, [_VP, ctypes.POINTER(GemmArgs)]),
     "mtk_attn_plan": (ctypes.c_int, [_VP, ctypes.POINTER(AttnDesc), _PP]),
     "mtk_attn_run": (ctypes.c_int, [_VP, ctypes.POINTER(AttnArgs)]),
+    "mtk_attn_bwd_plan": (ctypes.c_int, [_VP, ctypes.POINTER(AttnDesc), _PP]),
+    "mtk_attn_bwd_run": (ctypes.c_int, [_VP, ctypes.POINTER(AttnBwdArgs)]),
     "mtk_conv_plan": (ctypes.c_int, [_VP, ctypes.POINTER(ConvDesc), _PP]),
     "mtk_conv_out_shape": (ctypes.c_int, [ctypes.POINTER(ConvDesc)] + [ctypes.POINTER(ctypes.c_int)] * 3),
     "mtk_conv_run": (ctypes.c_int, [_VP, ctypes.POINTER(ConvArgs)]),
@@ -397,11 +404,33 @@ class AttentionPlan(_Plan):
         super().__init__(h)
 
     @staticmethod
-    def args(Q, K, V, O) -> AttnArgs:
-        return AttnArgs(Q=_ptr(Q), K=_ptr(K), V=_ptr(V), O=_ptr(O))
+    def args(Q, K, V, O, lse=None) -> AttnArgs:
+        return AttnArgs(Q=_ptr(Q), K=_ptr(K), V=_ptr(V), O=_ptr(O), lse=_ptr(lse))
 
-    def run(self, Q, K, V, O):
-        self._run(self.args(Q, K, V, O))
+    def run(self, Q, K, V, O, lse=None):
+        self._run(self.args(Q, K, V, O, lse))
+
+
+class AttentionBwdPlan(_Plan):
+    """dQ, dK, dV of the loss sum(dO * O) (Network.swift:313-402) from Q, K, V, the forward's O and
+    lse, and dO; tensors [B][S][H][D], lse [B][H][S_q] fp32; needs a workspace (the D vector)."""
+
+    _args_type = AttnBwdArgs
+    _run_fn = "mtk_attn_bwd_run"
+
+    def __init__(self, device: Device | None, B, H, S_q, S_kv, D=128, *, causal=False, dtype="f16"):
+        self.desc = AttnDesc(B=B, H=H, S_q=S_q, S_kv=S_kv, D=D, causal=1 if causal else 0, dtype=_DT[dtype], q_rows=0)
+        h = ctypes.c_void_p()
+        _check(lib().mtk_attn_bwd_plan(device.handle if device else None, ctypes.byref(self.desc), ctypes.byref(h)))
+        super().__init__(h)
+
+    @staticmethod
+    def args(Q, K, V, O, dO, lse, dQ, dK, dV, workspace) -> AttnBwdArgs:
+        return AttnBwdArgs(Q=_ptr(Q), K=_ptr(K), V=_ptr(V), O=_ptr(O), dO=_ptr(dO), lse=_ptr(lse), dQ=_ptr(dQ),
+                           dK=_ptr(dK), dV=_ptr(dV), workspace=_ptr(workspace))
+
+    def run(self, Q, K, V, O, dO, lse, dQ, dK, dV, workspace):
+        self._run(self.args(Q, K, V, O, dO, lse, dQ, dK, dV, workspace))
 
 
 def conv_desc(dims, has_bias=False, rank=None) -> ConvDesc:
@@ -468,19 +497,39 @@ def gemm(dev: Device, A, B, bias=None, *, trans_b=True, dtype="f16", split_k=1, 
     return out
 
 
-def attention(dev: Device, Q, K, V, *, causal=False, dtype="f16", q_rows=0) -> np.ndarray:
-    """attention.run equivalent on [B][S][H][D] tensors."""
+def attention(dev: Device, Q, K, V, *, causal=False, dtype="f16", q_rows=0, return_lse=False):
+    """attention.run equivalent on [B][S][H][D] tensors; with return_lse, also the [B][H][S_q]
+    fp32 row log-sum-exp the backward takes."""
     Q, K, V = _bits(Q), _bits(K), _bits(V)
     B, Sq, H, D = Q.shape
     plan = AttentionPlan(dev, B, H, Sq, K.shape[1], D, causal=causal, dtype=dtype, q_rows=q_rows)
     dQ, dK, dV = dev.upload(Q), dev.upload(K), dev.upload(V)
     dO = dev.empty(Q.nbytes)
-    plan.run(dQ, dK, dV, dO)
+    dl = dev.empty(B * H * Sq * 4) if return_lse else None
+    plan.run(dQ, dK, dV, dO, dl)
     dev.sync()
     out = dev.download(dO, Q.shape, Q.dtype)
-    for b in (dQ, dK, dV, dO):
+    lse = dev.download(dl, (B, H, Sq), np.float32) if return_lse else None
+    for b in (dQ, dK, dV, dO, dl):
+        if b is not None:
+            b.free()
+    return (out, lse) if return_lse else out
+
+
+def attention_bwd(dev: Device, Q, K, V, O, dO, lse, *, causal=False, dtype="f16"):
+    """(dQ, dK, dV) of the loss sum(dO * O) given the forward's O and lse (Network.swift:313-402)."""
+    Q, K, V, O, dO = _bits(Q), _bits(K), _bits(V), _bits(O), _bits(dO)
+    B, Sq, H, D = Q.shape
+    plan = AttentionBwdPlan(dev, B, H, Sq, K.shape[1], D, causal=causal, dtype=dtype)
+    bufs = [dev.upload(x) for x in (Q, K, V, O, dO, np.ascontiguousarray(lse, np.float32))]
+    outs = [dev.empty(x.nbytes) for x in (Q, K, V)]
+    ws = dev.empty(plan.workspace_bytes)
+    plan.run(*bufs, *outs, ws)
+    dev.sync()
+    res = tuple(dev.download(o, x.shape, x.dtype) for o, x in zip(outs, (Q, K, V)))
+    for b in bufs + outs + [ws]:
         b.free()
-    return out
+    return res
 
 
 def conv(dev: Device, dims, x, w, bias=None) -> np.ndarray:

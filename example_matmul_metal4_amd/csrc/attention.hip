@@ -49,6 +49,17 @@ __device__ __forceinline__ uint32_t k_off(int row, int chunk) {  // K tile: 64 r
   return (uint32_t)(row * 256 + ((chunk ^ (row & 15)) << 4));
 }
 
+// Row log-sum-exp for the backward (natural log of sum_j exp(s_ij * scale)): the exponent offset
+// m_off (log2 domain) plus log2 of the row sum, converted to natural log; -inf for a query that
+// sees no key. One lane of each lane pair (lane, lane ^ 32) writes.
+__device__ __forceinline__ void store_lse(const mtk_attn_kargs &a, int b, int h, int qi, int g, float m_off,
+                                          float l_tot) {
+  if (a.lse != nullptr && qi < a.S_q && g == 0) {
+    const float lse2 = l_tot > 0.0f ? m_off + __builtin_amdgcn_logf(l_tot) : -INFINITY;
+    a.lse[((size_t)b * a.H + h) * a.S_q + qi] = lse2 * 0.6931471805599453f;
+  }
+}
+
 template <int DT, bool CAUSAL>
 __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
   // K slots 0, 1 then V slots 0, 1
@@ -266,6 +277,7 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
   // ---- epilogue: O[qi][h][d] = O^T[d][qi] / l
   const float l_tot = half_sum(l_run);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  store_lse(a, b, h, qi, g, m_off, l_tot);
   if (qi < a.S_q) {
     uint16_t *O = (uint16_t *)a.O;
     const size_t obase = (((size_t)b * a.S_q + qi) * a.H + h) * kD;
@@ -539,6 +551,7 @@ __device__ __forceinline__ void attn_fwd_pp(const mtk_attn_kargs &a) {
 
   const float l_tot = half_sum(l_run);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  store_lse(a, b, h, qi, g, m_off, l_tot);
   if (qi < a.S_q) {
     uint16_t *O = (uint16_t *)a.O;
     const size_t obase = (((size_t)b * a.S_q + qi) * a.H + h) * kD;

@@ -1,0 +1,418 @@
+// Flash-attention backward for gfx950 (head dim 128), fp16/bf16 in and out, fp32 accumulate.
+//
+// The reference has no GPU backward; its CPU restatement of the gradients of the loss
+// Phi = sum dO * O is Sources/attention/Network.swift:205-281 (dP row, D-term, dS row) and
+// 313-402 (dV = P^T dO, dK = dS^T Q, dQ = dS K). These kernels compute the same quantities for
+// tensors laid out [B][S][H][D] (the forward's layout), with the causal mask of the forward:
+//   P  = exp(Q K^T * scale - lse)          (lse: the forward's row log-sum-exp, natural log)
+//   D  = rowsum(dO * O)                     (O: the forward's output)
+//   dS = P * (dO V^T - D) * scale
+//   dV = P^T dO,  dK = dS^T Q,  dQ = dS K
+// Three kernels, no atomics (every output element is written once, sums in a fixed order):
+//   attn_bwd_pre   D for every query row.
+//   attn_bwd_dkdv  one workgroup per 128 keys of one (batch, head), 4 wavefronts x 32 keys; the
+//                  query rows stream through LDS in tiles of 64. S = Q.K^T is computed with the
+//                  key as the accumulator column, Q rows fed in the order swap_bits_2_3(m) so that
+//                  accumulator registers 0-7 / 8-15 hold 8 consecutive queries: P and dS leave the
+//                  accumulators as the B operands of dV^T += dO^T.P and dK^T += Q^T.dS, whose
+//                  A operands are transposed LDS reads (ds_read_b64_tr_b16) of the dO / Q tiles.
+//   attn_bwd_dq    one workgroup per 256 queries, 8 wavefronts x 32 queries (the forward's shape):
+//                  S^T = K.Q^T and dP^T = V.dO^T with the query as the accumulator column, then
+//                  dQ^T += K^T.dS^T with K^T read transposed from LDS.
+// Each LDS operand tile is 64 rows of 256 bytes; tiles read as rows use the chunk swizzle
+// chunk ^ (row & 15), tiles read transposed chunk ^ 4 * (row & 3) (both conflict-free, as in the
+// forward); an operand read both ways is staged twice.
+#include "device.hpp"
+
+namespace mtk {
+
+constexpr int kBD = 128;                 // head dimension
+constexpr int kRowTile = 64 * kBD * 2;   // one 64-row operand tile in LDS: 16 KB
+constexpr int kBwdKeys = 128;            // keys per dK/dV workgroup
+constexpr int kBwdQTile = 64;            // queries per LDS tile of the dK/dV kernel
+constexpr int kBwdQRows = 256;           // queries per dQ workgroup
+constexpr int kBwdKTile = 64;            // keys per LDS tile of the dQ kernel
+
+__device__ __forceinline__ int bwd_swap_bits_2_3(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
+
+// Row-read tile: byte offset of 16-byte chunk `chunk` of row `row`.
+__device__ __forceinline__ uint32_t row_off(int row, int chunk) {
+  return (uint32_t)(row * 256 + ((chunk ^ (row & 15)) << 4));
+}
+
+// Transposed-read fragment base for d block db: lane (h = lane / 16, s = lane % 16) reads rows
+// 8 (h / 2) + s / 4 (+ 4 e, + 16 js) at d = 32 db + 16 (h & 1) + 4 (s & 3); the result is the A
+// operand [32 d][16 rows] of a 32x32x16 MFMA: lane gets d = 32 db + lane % 32 at rows
+// 16 js + 8 (lane / 32) + 0..7.
+__device__ __forceinline__ uint32_t tr_base(const char *tile, int db, int lane) {
+  const int s = lane & 15, h = lane >> 4;
+  const int d = 32 * db + 16 * (h & 1) + 4 * (s & 3);
+  const int row = 8 * (h >> 1) + (s >> 2);
+  return lds_addr(tile) + (uint32_t)(row * 256 + 16 * ((d >> 3) ^ (4 * (row & 3))) + 2 * (d & 7));
+}
+
+// Transposed fragment for row step js (16 rows) from a base made by tr_base (+ a tile offset).
+template <int JS>
+__device__ __forceinline__ u32x4 tr_frag(uint32_t base) {
+  const u32x2 w0 = ds_read_tr16_at<4096 * JS>(base);
+  const u32x2 w1 = ds_read_tr16_at<4096 * JS + 1024>(base);
+  return u32x4{w0.x, w0.y, w1.x, w1.y};
+}
+
+// Stage rows [row0, row0 + 4 * n) of a 64-row operand tile: instruction i fills 4 rows (1 KB),
+// lane l writes row row0 + 4 i + l / 16, LDS chunk l % 16, which holds global chunk
+// (l % 16) ^ swizzle(row). Rows at or past `rows_valid` read zero.
+template <int N, bool TR>
+__device__ __forceinline__ void stage_rows(rsrc_t r, char *tile, int row0, uint32_t base, uint32_t rs, int rows_valid,
+                                           int lane) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int row = row0 + 4 * i + (lane >> 4);
+    const int pc = lane & 15;
+    const int gc = TR ? (pc ^ (4 * (row & 3))) : (pc ^ (row & 15));
+    lds_direct16(r, tile + (row0 + 4 * i) * 256, row < rows_valid ? base + (uint32_t)row * rs + 16u * gc : kOOB);
+  }
+}
+
+// ------------------------------------------------------------------------------------- D-term
+
+template <int DT>
+__device__ __forceinline__ void attn_bwd_pre(const mtk_attn_bwd_kargs &a) {
+  // 16 lanes per (b, q, h) row of 128: lane loads 8 elements of O and dO
+  const long long row = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const long long rows = (long long)a.B * a.S_q * a.H;
+  if (row >= rows) return;
+  const int j = threadIdx.x & 15;
+  const rsrc_t ro = make_rsrc(a.O, a.q_bytes);
+  const rsrc_t rg = make_rsrc(a.dO, a.q_bytes);
+  const uint32_t off = (uint32_t)(row * kBD + 8 * j) * 2u;
+  const u32x4 o = buf_load16(ro, off), g = buf_load16(rg, off);
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    s = __builtin_fmaf(from_bits<DT>(o[e] & 0xffffu), from_bits<DT>(g[e] & 0xffffu), s);
+    s = __builtin_fmaf(from_bits<DT>(o[e] >> 16), from_bits<DT>(g[e] >> 16), s);
+  }
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m, 16);
+  if (j == 0) {
+    const int h = (int)(row % a.H);
+    const long long bq = row / a.H;
+    const int q = (int)(bq % a.S_q), b = (int)(bq / a.S_q);
+    a.Dt[((size_t)b * a.H + h) * a.S_q + q] = s;
+  }
+}
+
+// ------------------------------------------------------------------------------------- dK, dV
+
+template <int DT, bool CAUSAL>
+__device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
+  // per stage: Q rows, Q transposed-read copy, dO rows, dO transposed-read copy
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 4 * kRowTile];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..3
+  const int g = lane >> 5, col = lane & 31;
+
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = id / a.k_blocks;
+  const int kb = id - bh * a.k_blocks;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int k0 = kb * kBwdKeys;
+  const uint32_t rs = (uint32_t)a.H * kBD * 2;
+  const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kBD * 2);
+  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H + h) * kBD * 2);
+  const rsrc_t rq = make_rsrc(a.Q, a.q_bytes);
+  const rsrc_t rg = make_rsrc(a.dO, a.q_bytes);
+  const rsrc_t rk = make_rsrc(a.K, a.kv_bytes);
+  const rsrc_t rv = make_rsrc(a.V, a.kv_bytes);
+  const int diag = a.S_kv - a.S_q;  // key j is visible to query i iff j <= i + diag (causal)
+  const float c = a.scale_log2;
+
+  // this lane's key (accumulator column) and its K / V rows as B operands (8 steps of 16 dims)
+  const int key = k0 + wave * 32 + col;
+  const bool key_ok = key < a.S_kv;
+  u32x4 kf[8], vf[8];
+#pragma unroll
+  for (int ds = 0; ds < 8; ++ds) {
+    const uint32_t off = key_ok ? kvbase + (uint32_t)key * rs + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB;
+    kf[ds] = buf_load16(rk, off);
+    vf[ds] = buf_load16(rv, off);
+  }
+
+  // query tiles that see at least one of this workgroup's keys
+  int t0 = 0;
+  if (CAUSAL) t0 = max(0, k0 - diag) / kBwdQTile;
+  const int n_tiles = (a.S_q + kBwdQTile - 1) / kBwdQTile;
+
+  auto stage = [&](int slot, int t) {
+    char *st = smem + slot * 4 * kRowTile;
+    const int valid = a.S_q - t * kBwdQTile;
+    const uint32_t tb = qbase + (uint32_t)(t * kBwdQTile) * rs;
+    stage_rows<4, false>(rq, st, 16 * wave, tb, rs, valid, lane);
+    stage_rows<4, true>(rq, st + kRowTile, 16 * wave, tb, rs, valid, lane);
+    stage_rows<4, false>(rg, st + 2 * kRowTile, 16 * wave, tb, rs, valid, lane);
+    stage_rows<4, true>(rg, st + 3 * kRowTile, 16 * wave, tb, rs, valid, lane);
+  };
+
+  // A-operand rows of S = Q.K^T / dP = dO.V^T: MFMA row m reads query swap_bits_2_3(m) of the block
+  const int arow = bwd_swap_bits_2_3(col);
+  f32x16 dk[4], dv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    dk[i] = f32x16{};
+    dv[i] = f32x16{};
+  }
+
+  if (t0 < n_tiles) stage(t0 & 1, t0);
+  for (int t = t0; t < n_tiles; ++t) {
+    wait_vmem();
+    __syncthreads();  // tile t is in LDS; everyone is done with tile t-1's slot
+    if (t + 1 < n_tiles) stage((t + 1) & 1, t + 1);
+    const char *st = smem + (t & 1) * 4 * kRowTile;
+    const char *qrow = st, *qtr = st + kRowTile, *grow = st + 2 * kRowTile, *gtr = st + 3 * kRowTile;
+    const int qt0 = t * kBwdQTile;
+
+    // S and dP for the two 32-query blocks of the tile
+    f32x16 s[2], p[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      s[qb] = f32x16{};
+      p[qb] = f32x16{};
+#pragma unroll
+      for (int ds = 0; ds < 8; ++ds) {
+        const uint32_t o = row_off(32 * qb + arow, 2 * ds + g);
+        s[qb] = mfma32x32x16<DT>(*(const u32x4 *)(qrow + o), kf[ds], s[qb]);
+        p[qb] = mfma32x32x16<DT>(*(const u32x4 *)(grow + o), vf[ds], p[qb]);
+      }
+    }
+
+    // P and dS; register r of block qb is query qt0 + 32 qb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8)
+    u32x4 pb[4], sb[4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int q = qt0 + 32 * qb + 16 * half + 8 * g;  // first of 8 consecutive queries
+        float lse[8], dd[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const bool ok = q + e < a.S_q;
+          const size_t idx = ((size_t)b * a.H + h) * a.S_q + (size_t)(ok ? q + e : 0);
+          lse[e] = ok ? a.lse[idx] * 1.4426950408889634f : 0.0f;
+          dd[e] = ok ? a.Dt[idx] : 0.0f;
+        }
+        float pv[8], sv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int r = 8 * half + e;
+          const int qi = q + e;
+          const bool ok = key_ok && qi < a.S_q && (!CAUSAL || key <= qi + diag);
+          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][r], c, -lse[e]));
+          pv[e] = ok ? pe : 0.0f;
+          sv[e] = ok ? pe * (p[qb][r] - dd[e]) * a.scale : 0.0f;
+        }
+        const int js = 2 * qb + half;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pb[js][e] = pack2<DT>(pv[2 * e], pv[2 * e + 1]);
+          sb[js][e] = pack2<DT>(sv[2 * e], sv[2 * e + 1]);
+        }
+      }
+    }
+
+    // dV^T += dO^T . P and dK^T += Q^T . dS, d block by d block
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const uint32_t gbase = tr_base(gtr, db, lane), qbase_ = tr_base(qtr, db, lane);
+      u32x4 gf[4], qf[4];
+      static_for<0, 4>([&](auto jc) {
+        constexpr int JS = decltype(jc)::value;
+        gf[JS] = tr_frag<JS>(gbase);
+        qf[JS] = tr_frag<JS>(qbase_);
+      });
+      lgkm_wait0(gf);
+      lgkm_wait0(qf);
+#pragma unroll
+      for (int js = 0; js < 4; ++js) {
+        dv[db] = mfma32x32x16<DT>(gf[js], pb[js], dv[db]);
+        dk[db] = mfma32x32x16<DT>(qf[js], sb[js], dk[db]);
+      }
+    }
+  }
+
+  // dK[key][d], dV[key][d]: lane = key, register 4 rq + e of block db = d 32 db + 8 rq + 4 g + e
+  if (key_ok) {
+    uint16_t *dK = (uint16_t *)a.dK;
+    uint16_t *dV = (uint16_t *)a.dV;
+    const size_t base = (((size_t)b * a.S_kv + key) * a.H + h) * kBD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = db * 32 + 8 * rq + 4 * g;
+        *(u32x2 *)(dK + base + d) = u32x2{pack2<DT>(dk[db][4 * rq], dk[db][4 * rq + 1]),
+                                          pack2<DT>(dk[db][4 * rq + 2], dk[db][4 * rq + 3])};
+        *(u32x2 *)(dV + base + d) = u32x2{pack2<DT>(dv[db][4 * rq], dv[db][4 * rq + 1]),
+                                          pack2<DT>(dv[db][4 * rq + 2], dv[db][4 * rq + 3])};
+      }
+  }
+}
+
+// ------------------------------------------------------------------------------------- dQ
+
+template <int DT, bool CAUSAL>
+__device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
+  // per stage: K rows, K transposed-read copy, V rows
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 3 * kRowTile];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..7
+  const int g = lane >> 5, col = lane & 31;
+
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = id / a.q_blocks;
+  int qblk = id - bh * a.q_blocks;
+  if (CAUSAL) qblk = a.q_blocks - 1 - qblk;  // heaviest query blocks first
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int q0 = qblk * kBwdQRows;
+  const uint32_t rs = (uint32_t)a.H * kBD * 2;
+  const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kBD * 2);
+  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H + h) * kBD * 2);
+  const rsrc_t rq = make_rsrc(a.Q, a.q_bytes);
+  const rsrc_t rg = make_rsrc(a.dO, a.q_bytes);
+  const rsrc_t rk = make_rsrc(a.K, a.kv_bytes);
+  const rsrc_t rv = make_rsrc(a.V, a.kv_bytes);
+  const int diag = a.S_kv - a.S_q;
+  const float c = a.scale_log2;
+
+  // this lane's query (accumulator column): Q and dO rows as B operands, its lse and D
+  const int qi = q0 + wave * 32 + col;
+  const bool q_ok = qi < a.S_q;
+  u32x4 qf[8], gf[8];
+#pragma unroll
+  for (int ds = 0; ds < 8; ++ds) {
+    const uint32_t off = q_ok ? qbase + (uint32_t)qi * rs + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB;
+    qf[ds] = buf_load16(rq, off);
+    gf[ds] = buf_load16(rg, off);
+  }
+  const size_t ridx = ((size_t)b * a.H + h) * a.S_q + (size_t)(q_ok ? qi : 0);
+  const float lse2 = q_ok ? a.lse[ridx] * 1.4426950408889634f : 0.0f;
+  const float dterm = q_ok ? a.Dt[ridx] : 0.0f;
+
+  int kv_end = a.S_kv;
+  if (CAUSAL) kv_end = min(a.S_kv, q0 + kBwdQRows + diag);
+  const int n_tiles = kv_end > 0 ? (kv_end + kBwdKTile - 1) / kBwdKTile : 0;
+
+  auto stage = [&](int slot, int t) {
+    char *st = smem + slot * 3 * kRowTile;
+    const int valid = a.S_kv - t * kBwdKTile;
+    const uint32_t tb = kvbase + (uint32_t)(t * kBwdKTile) * rs;
+    stage_rows<2, false>(rk, st, 8 * wave, tb, rs, valid, lane);
+    stage_rows<2, true>(rk, st + kRowTile, 8 * wave, tb, rs, valid, lane);
+    stage_rows<2, false>(rv, st + 2 * kRowTile, 8 * wave, tb, rs, valid, lane);
+  };
+
+  const int arow = bwd_swap_bits_2_3(col);  // MFMA row m reads key swap_bits_2_3(m) of the block
+  f32x16 dq[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dq[i] = f32x16{};
+
+  if (n_tiles > 0) stage(0, 0);
+  for (int t = 0; t < n_tiles; ++t) {
+    wait_vmem();
+    __syncthreads();  // tile t is in LDS; everyone is done with tile t-1's slot
+    if (t + 1 < n_tiles) stage((t + 1) & 1, t + 1);
+    const char *st = smem + (t & 1) * 3 * kRowTile;
+    const char *krow = st, *ktr = st + kRowTile, *vrow = st + 2 * kRowTile;
+    const int j0 = t * kBwdKTile;
+
+    // S^T and dP^T for the two 32-key blocks of the tile
+    f32x16 s[2], p[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      s[kb] = f32x16{};
+      p[kb] = f32x16{};
+#pragma unroll
+      for (int ds = 0; ds < 8; ++ds) {
+        const uint32_t o = row_off(32 * kb + arow, 2 * ds + g);
+        s[kb] = mfma32x32x16<DT>(*(const u32x4 *)(krow + o), qf[ds], s[kb]);
+        p[kb] = mfma32x32x16<DT>(*(const u32x4 *)(vrow + o), gf[ds], p[kb]);
+      }
+    }
+
+    // dS^T; register r of block kb is key j0 + 32 kb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8)
+    u32x4 sb[4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        float sv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int r = 8 * half + e;
+          const int kj = j0 + 32 * kb + 16 * half + 8 * g + e;
+          const bool ok = q_ok && kj < a.S_kv && (!CAUSAL || kj <= qi + diag);
+          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], c, -lse2));
+          sv[e] = ok ? pe * (p[kb][r] - dterm) * a.scale : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sb[2 * kb + half][e] = pack2<DT>(sv[2 * e], sv[2 * e + 1]);
+      }
+    }
+
+    // dQ^T += K^T . dS^T, d block by d block
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const uint32_t kbase_ = tr_base(ktr, db, lane);
+      u32x4 kt[4];
+      static_for<0, 4>([&](auto jc) {
+        constexpr int JS = decltype(jc)::value;
+        kt[JS] = tr_frag<JS>(kbase_);
+      });
+      lgkm_wait0(kt);
+#pragma unroll
+      for (int js = 0; js < 4; ++js) dq[db] = mfma32x32x16<DT>(kt[js], sb[js], dq[db]);
+    }
+  }
+
+  // dQ[qi][d]: lane = query, register 4 rq + e of block db = d 32 db + 8 rq + 4 g + e
+  if (q_ok) {
+    uint16_t *dQ = (uint16_t *)a.dQ;
+    const size_t base = (((size_t)b * a.S_q + qi) * a.H + h) * kBD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = db * 32 + 8 * rq + 4 * g;
+        *(u32x2 *)(dQ + base + d) = u32x2{pack2<DT>(dq[db][4 * rq], dq[db][4 * rq + 1]),
+                                          pack2<DT>(dq[db][4 * rq + 2], dq[db][4 * rq + 3])};
+      }
+  }
+}
+
+}  // namespace mtk
+
+using namespace mtk;
+
+#define BWD_PRE(NAME, DT) \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const mtk_attn_bwd_kargs a) { attn_bwd_pre<DT>(a); }
+#define BWD_DKDV(NAME, DT, CAUSAL)                                                   \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const mtk_attn_bwd_kargs a) { \
+    attn_bwd_dkdv<DT, CAUSAL>(a);                                                    \
+  }
+#define BWD_DQ(NAME, DT, CAUSAL)                                                     \
+  extern "C" __global__ void __launch_bounds__(512) NAME(const mtk_attn_bwd_kargs a) { \
+    attn_bwd_dq<DT, CAUSAL>(a);                                                      \
+  }
+
+BWD_PRE(mtk_attn_bwd_pre_f16, DT_F16)
+BWD_PRE(mtk_attn_bwd_pre_bf16, DT_BF16)
+BWD_DKDV(mtk_attn_bwd_dkdv_f16, DT_F16, false)
+BWD_DKDV(mtk_attn_bwd_dkdv_bf16, DT_BF16, false)
+BWD_DKDV(mtk_attn_bwd_dkdv_f16_causal, DT_F16, true)
+BWD_DKDV(mtk_attn_bwd_dkdv_bf16_causal, DT_BF16, true)
+BWD_DQ(mtk_attn_bwd_dq_f16, DT_F16, false)
+BWD_DQ(mtk_attn_bwd_dq_bf16, DT_BF16, false)
+BWD_DQ(mtk_attn_bwd_dq_f16_causal, DT_F16, true)
+BWD_DQ(mtk_attn_bwd_dq_bf16_causal, DT_BF16, true)

@@ -9,7 +9,7 @@
 
 #include <stdint.h>
 
-#define MTK_KARGS_VERSION 4
+#define MTK_KARGS_VERSION 5
 
 /* Tile-GEMM kernels: plain GEMM (A [M][K] . B, B either [N][K] or [K][N]) and
  * implicit-GEMM convolution (A = im2col of an NDHWC activation, B = DHWIO
@@ -87,6 +87,22 @@ typedef struct {
   int32_t causal;
   float scale_log2; /* log2(e) / sqrt(D) */
   uint32_t q_bytes, kv_bytes;
+  float *lse; /* [B][H][S_q] natural-log row log-sum-exp of the scaled scores, or NULL */
 } mtk_attn_kargs;
+
+/* Flash-attention backward (all three kernels of the plan take this block). */
+typedef struct {
+  const void *Q, *K, *V, *O, *dO;
+  const float *lse; /* [B][H][S_q] from the forward */
+  float *Dt;        /* [B][H][S_q] workspace: rowsum(dO * O) */
+  void *dQ, *dK, *dV;
+  int32_t B, H, S_q, S_kv;
+  int32_t q_blocks; /* ceil(S_q / 256): dQ workgroups per (batch, head) */
+  int32_t k_blocks; /* ceil(S_kv / 128): dK/dV workgroups per (batch, head) */
+  int32_t causal;
+  float scale_log2; /* log2(e) / sqrt(D) */
+  float scale;      /* 1 / sqrt(D) */
+  uint32_t q_bytes, kv_bytes;
+} mtk_attn_bwd_kargs;
 
 #endif

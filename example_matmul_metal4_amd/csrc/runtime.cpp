@@ -81,7 +81,7 @@ struct mtk_ctx {
 
 namespace {
 
-enum PlanKind { PLAN_GEMM = 1, PLAN_ATTN = 2, PLAN_CONV = 3 };
+enum PlanKind { PLAN_GEMM = 1, PLAN_ATTN = 2, PLAN_CONV = 3, PLAN_ATTN_BWD = 4 };
 
 enum LaunchRole { ROLE_MAIN = 0, ROLE_REDUCE = 1 };
 
@@ -369,6 +369,76 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   return MTK_OK;
 }
 
+// Attention backward: D-term pass, then dK/dV (one workgroup per 128 keys) and dQ (one per 256
+// queries), all reading the forward's lse; the D vector lives in the plan's workspace.
+int plan_attn_bwd(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
+  if (!d_in || !out) return fail(MTK_ERR_INVALID, "null descriptor or output");
+  mtk_attn_desc d = *d_in;
+  if (d.B <= 0 || d.H <= 0 || d.S_q <= 0 || d.S_kv <= 0) return fail(MTK_ERR_INVALID, "B, H, S_q, S_kv must be positive");
+  if (d.D != 128) return fail(MTK_ERR_UNSUPPORTED, "head dimension must be 128 (got %d)", d.D);
+  if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "attention dtype must be MTK_F16 or MTK_BF16");
+  if (d.q_rows != 0) return fail(MTK_ERR_INVALID, "the backward plan chooses its own blocking (q_rows must be 0)");
+  const uint64_t q_bytes = (uint64_t)d.B * d.S_q * d.H * d.D * 2;
+  const uint64_t kv_bytes = (uint64_t)d.B * d.S_kv * d.H * d.D * 2;
+  if (q_bytes > kMaxOperandBytes || kv_bytes > kMaxOperandBytes)
+    return fail(MTK_ERR_UNSUPPORTED, "operands above 2 GiB are not supported by this build");
+  mtk_plan *p = new mtk_plan();
+  p->ctx = ctx;
+  p->kind = PLAN_ATTN_BWD;
+  p->attn = d;
+  p->align_a = p->align_b = 16;
+  const char *dt = d.dtype == MTK_F16 ? "f16" : "bf16";
+  const char *cz = d.causal ? "_causal" : "";
+  mtk_attn_bwd_kargs a{};
+  a.B = d.B;
+  a.H = d.H;
+  a.S_q = d.S_q;
+  a.S_kv = d.S_kv;
+  a.q_blocks = (d.S_q + 255) / 256;
+  a.k_blocks = (d.S_kv + 127) / 128;
+  a.causal = d.causal ? 1 : 0;
+  a.scale = (float)(1.0 / std::sqrt((double)d.D));
+  a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)d.D));
+  a.q_bytes = (uint32_t)q_bytes;
+  a.kv_bytes = (uint32_t)kv_bytes;
+  Launch pre, kv, q;
+  pre.name = std::string("mtk_attn_bwd_pre_") + dt;
+  pre.grid = (unsigned)(((long long)d.B * d.S_q * d.H + 15) / 16);
+  kv.name = std::string("mtk_attn_bwd_dkdv_") + dt + cz;
+  kv.grid = (unsigned)((long long)a.k_blocks * d.B * d.H);
+  q.name = std::string("mtk_attn_bwd_dq_") + dt + cz;
+  q.grid = (unsigned)((long long)a.q_blocks * d.B * d.H);
+  q.block = 512;
+  for (Launch *l : {&pre, &kv, &q}) {
+    set_args(*l, a);
+    p->launches.push_back(*l);
+  }
+  p->workspace = ((size_t)d.B * d.H * d.S_q * sizeof(float) + 255) & ~(size_t)255;
+  double pairs = (double)d.S_q * d.S_kv;
+  if (d.causal) {
+    pairs = 0;
+    for (long long i = 0; i < d.S_q; ++i) {
+      long long lim = i + (d.S_kv - d.S_q) + 1;
+      pairs += (double)std::max(0ll, std::min<long long>(lim, d.S_kv));
+    }
+  }
+  // five products of 2 * pairs * D flops each (S, dP, dV, dK, dQ; the dQ kernel's recomputation of
+  // S and dP is not counted); bytes: Q, K, V, O, dO read, dQ, dK, dV written, lse and D
+  p->flops = 10.0 * d.B * d.H * d.D * pairs;
+  p->bytes = 4.0 * (double)q_bytes + 4.0 * (double)kv_bytes + 3.0 * 4.0 * d.B * d.H * d.S_q;
+  char desc[256];
+  snprintf(desc, sizeof desc, "attention bwd %s B=%d H=%d S_q=%d S_kv=%d D=%d causal=%d grids=%u/%u/%u", dt, d.B,
+           d.H, d.S_q, d.S_kv, d.D, d.causal, pre.grid, kv.grid, q.grid);
+  p->description = desc;
+  int s = resolve(p);
+  if (s != MTK_OK) {
+    delete p;
+    return s;
+  }
+  *out = p;
+  return MTK_OK;
+}
+
 // ------------------------------------------------------------------ conv planning
 
 int conv_out(const mtk_conv_desc *d, int *od, int *oh, int *ow) {
@@ -630,16 +700,40 @@ int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
     a.bias = c->bias;
     a.C = c->y;
     a.partial = nullptr;
+  } else if (p->kind == PLAN_ATTN_BWD) {
+    const mtk_attn_bwd_args *t = (const mtk_attn_bwd_args *)argset;
+    if (!t || !t->Q || !t->K || !t->V || !t->O || !t->dO || !t->lse || !t->dQ || !t->dK || !t->dV)
+      return fail(MTK_ERR_INVALID, "Q, K, V, O, dO, lse, dQ, dK and dV must be non-null");
+    for (const void *x : {t->Q, t->K, t->V, t->O, t->dO, (const void *)t->dQ, (const void *)t->dK, (const void *)t->dV})
+      if (!aligned(x, 16)) return fail(MTK_ERR_INVALID, "attention tensors must be 16-byte aligned");
+    if (!aligned(t->lse, 4)) return fail(MTK_ERR_INVALID, "lse must be 4-byte aligned");
+    if (!t->workspace || !aligned(t->workspace, 16))
+      return fail(MTK_ERR_INVALID, "this plan needs a 16-byte aligned workspace of %zu bytes", p->workspace);
+    for (Launch &l : ls) {
+      mtk_attn_bwd_kargs &a = args_of<mtk_attn_bwd_kargs>(l);
+      a.Q = t->Q;
+      a.K = t->K;
+      a.V = t->V;
+      a.O = t->O;
+      a.dO = t->dO;
+      a.lse = t->lse;
+      a.Dt = (float *)t->workspace;
+      a.dQ = t->dQ;
+      a.dK = t->dK;
+      a.dV = t->dV;
+    }
   } else {
     const mtk_attn_args *t = (const mtk_attn_args *)argset;
     if (!t || !t->Q || !t->K || !t->V || !t->O) return fail(MTK_ERR_INVALID, "Q, K, V and O must be non-null");
     if (!aligned(t->Q, 16) || !aligned(t->K, 16) || !aligned(t->V, 16) || !aligned(t->O, 16))
       return fail(MTK_ERR_INVALID, "Q, K, V, O must be 16-byte aligned");
+    if (t->lse && !aligned(t->lse, 4)) return fail(MTK_ERR_INVALID, "lse must be 4-byte aligned");
     mtk_attn_kargs &a = args_of<mtk_attn_kargs>(ls[0]);
     a.Q = t->Q;
     a.K = t->K;
     a.V = t->V;
     a.O = t->O;
+    a.lse = t->lse;
   }
   return MTK_OK;
 }
@@ -650,6 +744,8 @@ size_t argset_size(const mtk_plan *p) {
       return sizeof(mtk_gemm_args);
     case PLAN_CONV:
       return sizeof(mtk_conv_args);
+    case PLAN_ATTN_BWD:
+      return sizeof(mtk_attn_bwd_args);
     default:
       return sizeof(mtk_attn_args);
   }
@@ -879,6 +975,14 @@ int mtk_gemm_run(const mtk_plan *plan, const mtk_gemm_args *args) {
 int mtk_attn_plan(mtk_ctx *ctx, const mtk_attn_desc *desc, mtk_plan **out) { return plan_attn(ctx, desc, out); }
 int mtk_attn_run(const mtk_plan *plan, const mtk_attn_args *args) {
   if (plan && plan->kind != PLAN_ATTN) return fail(MTK_ERR_INVALID, "not an attention plan");
+  return run_plan(plan, args);
+}
+
+int mtk_attn_bwd_plan(mtk_ctx *ctx, const mtk_attn_desc *desc, mtk_plan **out) {
+  return plan_attn_bwd(ctx, desc, out);
+}
+int mtk_attn_bwd_run(const mtk_plan *plan, const mtk_attn_bwd_args *args) {
+  if (plan && plan->kind != PLAN_ATTN_BWD) return fail(MTK_ERR_INVALID, "not an attention backward plan");
   return run_plan(plan, args);
 }
 

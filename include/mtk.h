@@ -177,11 +177,35 @@ int mtk_attn_plan(mtk_ctx *ctx, const mtk_attn_desc *desc, mtk_plan **out);
 typedef struct {
   const void *Q, *K, *V;
   void *O;
+  /* appended: [B][H][S_q] fp32 natural-log log-sum-exp of each query's scaled scores
+   * (lse_i = log sum_j exp(q_i . k_j / sqrt(D)), -inf for a query that sees no key), written when
+   * not NULL: the backward's input. The reference keeps it in threadgroup memory only
+   * (attention.swift:166, 350-352). */
+  float *lse;
 } mtk_attn_args;
 
 /* Replaces setBuffer(0..3) + setThreadgroupMemoryLength + dispatchThreadgroups
  * (attention.swift:478-501). */
 int mtk_attn_run(const mtk_plan *plan, const mtk_attn_args *args);
+
+/* Attention backward: gradients of the loss sum(dO * O) with respect to Q, K and V, the quantities
+ * the reference computes on the CPU in Sources/attention/Network.swift:205-281, 313-402
+ * (derivativeQ / derivativeK / derivativeV) and has no GPU kernel for:
+ *   P = exp(Q K^T / sqrt(D) - lse), D_i = sum_d dO_id O_id, dS = P (dO V^T - D) / sqrt(D),
+ *   dV = P^T dO, dK = dS^T Q, dQ = dS K.
+ * Same descriptor as the forward (q_rows must be 0); same layouts; causal as in the forward. The
+ * plan needs a workspace of mtk_plan_workspace_bytes (the D vector). Deterministic: no atomics. */
+int mtk_attn_bwd_plan(mtk_ctx *ctx, const mtk_attn_desc *desc, mtk_plan **out);
+
+typedef struct {
+  const void *Q, *K, *V, *O, *dO; /* O: the forward's output for these Q, K, V */
+  const float *lse;               /* the forward's lse output */
+  void *dQ, *dK, *dV;             /* same shapes and dtype as Q, K, V */
+  void *workspace;                /* >= mtk_plan_workspace_bytes(plan), 16-byte aligned */
+} mtk_attn_bwd_args;
+
+/* Enqueues the three kernels (D-term, dK/dV, dQ). */
+int mtk_attn_bwd_run(const mtk_plan *plan, const mtk_attn_bwd_args *args);
 
 /* ------------------------------------------------------------------ convolution */
 
@@ -234,7 +258,7 @@ int mtk_plan_destroy(mtk_plan *plan);
  * gpuStartTime/gpuEndTime measurement (ConvolutionShared.swift:237-247, 2522-2539; matmul.swift:480-489).
  * Runs `warmup` untimed iterations, then `iters` timed ones, cycling through `nsets` argument sets
  * (so a large operand can be rotated to defeat the 256 MB Infinity Cache). Each set is the op's
- * args struct (mtk_gemm_args / mtk_attn_args / mtk_conv_args). HIP events on the plan's stream
+ * args struct (mtk_gemm_args / mtk_attn_args / mtk_attn_bwd_args / mtk_conv_args). HIP events on the plan's stream
  * bracket each kernel; results are averages per iteration, in milliseconds. */
 typedef struct {
   double total_ms;      /* per iteration, first launch start to last launch end */
