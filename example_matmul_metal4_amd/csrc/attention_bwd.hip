@@ -107,8 +107,10 @@ __device__ __forceinline__ void attn_bwd_pre(const mtk_attn_bwd_kargs &a) {
 
 template <int DT, bool CAUSAL>
 __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
-  // per stage: Q rows, Q transposed-read copy, dO rows, dO transposed-read copy
-  __shared__ __attribute__((aligned(1024))) char smem[2 * 4 * kRowTile];
+  // per stage: Q rows, Q transposed-read copy, dO rows, dO transposed-read copy, then the tile's
+  // 64 lse and 64 D values (1 KB slots, filled by one direct-to-LDS instruction each)
+  constexpr int kStageBytes = 4 * kRowTile + 2 * 1024;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStageBytes];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..3
@@ -126,6 +128,10 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   const rsrc_t rg = make_rsrc(a.dO, a.q_bytes);
   const rsrc_t rk = make_rsrc(a.K, a.kv_bytes);
   const rsrc_t rv = make_rsrc(a.V, a.kv_bytes);
+  const uint32_t row_bytes = (uint32_t)a.B * a.H * a.S_q * 4u;  // lse and D: [B][H][S_q] fp32
+  const rsrc_t rl = make_rsrc(a.lse, row_bytes);
+  const rsrc_t rd = make_rsrc(a.Dt, row_bytes);
+  const uint32_t row_base = (uint32_t)(((size_t)b * a.H + h) * a.S_q) * 4u;
   const int diag = a.S_kv - a.S_q;  // key j is visible to query i iff j <= i + diag (causal)
   const float c = a.scale_log2;
 
@@ -146,13 +152,19 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   const int n_tiles = (a.S_q + kBwdQTile - 1) / kBwdQTile;
 
   auto stage = [&](int slot, int t) {
-    char *st = smem + slot * 4 * kRowTile;
+    char *st = smem + slot * kStageBytes;
     const int valid = a.S_q - t * kBwdQTile;
     const uint32_t tb = qbase + (uint32_t)(t * kBwdQTile) * rs;
     stage_rows<4, false>(rq, st, 16 * wave, tb, rs, valid, lane);
     stage_rows<4, true>(rq, st + kRowTile, 16 * wave, tb, rs, valid, lane);
     stage_rows<4, false>(rg, st + 2 * kRowTile, 16 * wave, tb, rs, valid, lane);
     stage_rows<4, true>(rg, st + 3 * kRowTile, 16 * wave, tb, rs, valid, lane);
+    // lse (wave 0) and D (wave 1) of the tile's queries: lanes 0-15 load 4 values each (entries past
+    // S_q are never used unmasked); lanes 16-63 write zeros
+    if (wave < 2) {
+      const uint32_t off = lane < 16 ? row_base + (uint32_t)(t * kBwdQTile + 4 * lane) * 4u : kOOB;
+      lds_direct16(wave == 0 ? rl : rd, st + 4 * kRowTile + wave * 1024, off);
+    }
   };
 
   // A-operand rows of S = Q.K^T / dP = dO.V^T: MFMA row m reads query swap_bits_2_3(m) of the block
@@ -169,8 +181,9 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     wait_vmem();
     __syncthreads();  // tile t is in LDS; everyone is done with tile t-1's slot
     if (t + 1 < n_tiles) stage((t + 1) & 1, t + 1);
-    const char *st = smem + (t & 1) * 4 * kRowTile;
+    const char *st = smem + (t & 1) * kStageBytes;
     const char *qrow = st, *qtr = st + kRowTile, *grow = st + 2 * kRowTile, *gtr = st + 3 * kRowTile;
+    const float *lse_t = (const float *)(st + 4 * kRowTile), *d_t = (const float *)(st + 4 * kRowTile + 1024);
     const int qt0 = t * kBwdQTile;
 
     // S and dP for the two 32-query blocks of the tile
@@ -193,14 +206,19 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     for (int qb = 0; qb < 2; ++qb) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        const int q = qt0 + 32 * qb + 16 * half + 8 * g;  // first of 8 consecutive queries
+        const int qr = 32 * qb + 16 * half + 8 * g;  // first of 8 consecutive queries of the tile
+        const int q = qt0 + qr;
         float lse[8], dd[8];
+        {
+          const f32x4 l0 = *(const f32x4 *)(lse_t + qr), l1 = *(const f32x4 *)(lse_t + qr + 4);
+          const f32x4 d0 = *(const f32x4 *)(d_t + qr), d1 = *(const f32x4 *)(d_t + qr + 4);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const bool ok = q + e < a.S_q;
-          const size_t idx = ((size_t)b * a.H + h) * a.S_q + (size_t)(ok ? q + e : 0);
-          lse[e] = ok ? a.lse[idx] * 1.4426950408889634f : 0.0f;
-          dd[e] = ok ? a.Dt[idx] : 0.0f;
+          for (int e = 0; e < 4; ++e) {
+            lse[e] = l0[e] * 1.4426950408889634f;
+            lse[4 + e] = l1[e] * 1.4426950408889634f;
+            dd[e] = d0[e];
+            dd[4 + e] = d1[e];
+          }
         }
         float pv[8], sv[8];
 #pragma unroll
