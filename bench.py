@@ -20,7 +20,8 @@ published dense fp16 MFMA rate (2.5 PFLOP/s). ``traffic`` comes from the committ
 accumulation, OpenMP over rows) timed on this host on a bounded row sample of the same GEMM.
 
 ``configs``: every other BASELINE configuration measured the same way (split-K 1 variant of
-config 2, the bf16 decode GEMM in GB/s, conv2d / conv3d, flash attention fwd both masks).
+config 2, the bf16 decode GEMM in GB/s, conv2d / conv3d, flash attention fwd both masks), plus the
+attention backward at the config 5 shape.
 """
 from __future__ import annotations
 
@@ -271,6 +272,22 @@ def main():
                 s["reference_convention_tflops"] = (2 * 128 + 5) * 4096 * 4096 * 32 * 2 / (
                     2 if causal else 1) / (tm[0] * 1e-3) / 1e12
                 cfgs["config5_attn_causal" if causal else "config5_attn"] = s
+                # backward of the same shape (the reference's Network.swift gradients): O and lse from
+                # this forward, dO ~ N(0,1); FLOPs = five products of 2 S^2 D per (b, h)
+                pb = mtk.AttentionBwdPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
+                ws_b = dev.empty(pb.workspace_bytes)
+                grads = [dev.empty(int(np.prod(shp)) * 2) for _ in range(3)]
+                sets_b = []
+                for c, sa in enumerate(sets_a):
+                    o_c, lse_c = dev.empty(int(np.prod(shp)) * 2), dev.empty(2 * 32 * 4096 * 4)
+                    pa.run(sa.Q, sa.K, sa.V, o_c, lse_c)
+                    sets_b.append(pb.args(sa.Q, sa.K, sa.V, o_c, dev.upload(inputs.normal(13 + 100 * c, shp)), lse_c,
+                                          *grads, ws_b))
+                dev.sync()
+                tm = time_steps(dev, pb, sets_b, args.warmup, steps)
+                cfgs["config5_attn_bwd_causal" if causal else "config5_attn_bwd"] = summarize(
+                    f"config 5 shape, flash-attn backward (dQ, dK, dV) {'causal' if causal else 'non-causal'}", pb, tm,
+                    "mfma", key="config5_bwd_causal" if causal else "config5_bwd")
         except Exception as e:  # report what was measured; the headline stands on its own
             cfgs["error"] = repr(e)
         line["configs"] = cfgs

@@ -8,7 +8,7 @@ once; only the plan's kernels run in the loop.
 
 Cases: gemm (config 2, 4096 x 4096 x 4100 + bias, B [N][K]), gemm_nn (4096^3, B [K][N]), decode
 (config 3, bf16 M=16, 3 rotating input copies), conv2d / conv3d (config 4), attn / attn_causal
-(config 5), copy (torch's device-to-device copy of 256 MiB: known HBM traffic of 256 MiB read and
+(config 5), attn_bwd / attn_bwd_causal (the backward at the config 5 shape), copy (torch's device-to-device copy of 256 MiB: known HBM traffic of 256 MiB read and
 256 MiB written per launch, used to scale the FETCH_SIZE / WRITE_SIZE counters).
 """
 import argparse
@@ -19,7 +19,8 @@ import numpy as np
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
-    ap.add_argument("case", choices=["gemm", "gemm_nn", "decode", "conv2d", "conv3d", "attn", "attn_causal", "copy"])
+    ap.add_argument("case", choices=["gemm", "gemm_nn", "decode", "conv2d", "conv3d", "attn", "attn_causal", "attn_bwd",
+                                     "attn_bwd_causal", "copy"])
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--split", type=int, default=4)
     ap.add_argument("--tile", type=int, default=0)
@@ -82,6 +83,16 @@ def main(argv=None):
             sets = [plan.args(dev.upload(inputs.uniform(7, xs, -1, 1)), dev.upload(inputs.uniform(8, wsh, -1, 1)),
                               dev.upload(inputs.uniform(9, (desc.O,), -1, 1)),
                               dev.empty(int(np.prod(plan.out_shape())) * 2))]
+        elif a.case in ("attn_bwd", "attn_bwd_causal"):
+            causal = a.case == "attn_bwd_causal"
+            shp = (2, 4096, 32, 128)
+            fwd = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
+            q, k, v = (dev.upload(inputs.normal(s, shp)) for s in (10, 11, 12))
+            o, lse = dev.empty(int(np.prod(shp)) * 2), dev.empty(2 * 32 * 4096 * 4)
+            fwd.run(q, k, v, o, lse)
+            plan = mtk.AttentionBwdPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
+            sets = [plan.args(q, k, v, o, dev.upload(inputs.normal(13, shp)), lse,
+                              *(dev.empty(int(np.prod(shp)) * 2) for _ in range(3)), dev.empty(plan.workspace_bytes))]
         else:
             plan = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, causal=a.case == "attn_causal", q_rows=a.rows)
             shp = (2, 4096, 32, 128)
