@@ -106,6 +106,14 @@ class ConvArgs(ctypes.Structure):
                 ("workspace", ctypes.c_void_p)]
 
 
+class PermuteDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("O", "C", "KD", "KH", "KW")]
+
+
+class PermuteArgs(ctypes.Structure):
+    _fields_ = [("src", ctypes.c_void_p), ("dst", ctypes.c_void_p)]
+
+
 class Timing(ctypes.Structure):
     _fields_ = [("total_ms", ctypes.c_double), ("kernel_ms", ctypes.c_double * 4), ("n_kernels", ctypes.c_int),
                 ("kernel_names", (ctypes.c_char * 64) * 4)]
@@ -146,6 +154,8 @@ SIGNATURES = {
     "mtk_conv_plan": (ctypes.c_int, [_VP, ctypes.POINTER(ConvDesc), _PP]),
     "mtk_conv_out_shape": (ctypes.c_int, [ctypes.POINTER(ConvDesc)] + [ctypes.POINTER(ctypes.c_int)] * 3),
     "mtk_conv_run": (ctypes.c_int, [_VP, ctypes.POINTER(ConvArgs)]),
+    "mtk_permute_plan": (ctypes.c_int, [_VP, ctypes.POINTER(PermuteDesc), _PP]),
+    "mtk_permute_run": (ctypes.c_int, [_VP, ctypes.POINTER(PermuteArgs)]),
     "mtk_plan_workspace_bytes": (ctypes.c_size_t, [_VP]),
     "mtk_plan_describe": (ctypes.c_int, [_VP, ctypes.c_char_p, ctypes.c_size_t]),
     "mtk_plan_work": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
@@ -431,6 +441,44 @@ class AttentionBwdPlan(_Plan):
 
     def run(self, Q, K, V, O, dO, lse, dQ, dK, dV, workspace):
         self._run(self.args(Q, K, V, O, dO, lse, dQ, dK, dV, workspace))
+
+
+class PermutePlan(_Plan):
+    """OIDHW -> DHWIO weight re-layout (WeightPermutationSession3D, ConvolutionShared.swift:1577-1674):
+    dst[kd][kh][kw][c][o] = src[o][c][kd][kh][kw] for 16-bit elements."""
+
+    _args_type = PermuteArgs
+    _run_fn = "mtk_permute_run"
+
+    def __init__(self, device: Device | None, O, C, KD, KH, KW):
+        self.desc = PermuteDesc(O=O, C=C, KD=KD, KH=KH, KW=KW)
+        h = ctypes.c_void_p()
+        _check(lib().mtk_permute_plan(device.handle if device else None, ctypes.byref(self.desc), ctypes.byref(h)))
+        super().__init__(h)
+
+    @staticmethod
+    def args(src, dst) -> PermuteArgs:
+        return PermuteArgs(src=_ptr(src), dst=_ptr(dst))
+
+    def run(self, src, dst):
+        self._run(self.args(src, dst))
+
+
+def permute_oidhw_to_dhwio(dev: Device, w) -> np.ndarray:
+    """[O][C][KD][KH][KW] (or [O][C][KH][KW]) 16-bit weights -> [KD][KH][KW][C][O] on the GPU."""
+    w = _bits(w)
+    if w.ndim == 4:
+        w = w.reshape(w.shape[0], w.shape[1], 1, w.shape[2], w.shape[3])
+    O, C, KD, KH, KW = w.shape
+    plan = PermutePlan(dev, O, C, KD, KH, KW)
+    src = dev.upload(w)
+    dst = dev.empty(w.nbytes)
+    plan.run(src, dst)
+    dev.sync()
+    out = dev.download(dst, (KD, KH, KW, C, O), w.dtype)
+    src.free()
+    dst.free()
+    return out
 
 
 def conv_desc(dims, has_bias=False, rank=None) -> ConvDesc:

@@ -9,7 +9,7 @@
 
 #include <stdint.h>
 
-#define MTK_KARGS_VERSION 5
+#define MTK_KARGS_VERSION 6
 
 /* Tile-GEMM kernels: plain GEMM (A [M][K] . B, B either [N][K] or [K][N]) and
  * implicit-GEMM convolution (A = im2col of an NDHWC activation, B = DHWIO
@@ -104,5 +104,12 @@ typedef struct {
   float scale;      /* 1 / sqrt(D) */
   uint32_t q_bytes, kv_bytes;
 } mtk_attn_bwd_kargs;
+
+/* Convolution weight re-layout OIDHW -> DHWIO (16-bit elements). */
+typedef struct {
+  const void *src; /* [O][C][KD][KH][KW] */
+  void *dst;       /* [KD][KH][KW][C][O] */
+  int32_t O, C, T; /* T = KD * KH * KW */
+} mtk_permute_args;
 
 #endif

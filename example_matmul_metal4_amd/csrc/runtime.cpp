@@ -81,7 +81,7 @@ struct mtk_ctx {
 
 namespace {
 
-enum PlanKind { PLAN_GEMM = 1, PLAN_ATTN = 2, PLAN_CONV = 3, PLAN_ATTN_BWD = 4 };
+enum PlanKind { PLAN_GEMM = 1, PLAN_ATTN = 2, PLAN_CONV = 3, PLAN_ATTN_BWD = 4, PLAN_PERMUTE = 5 };
 
 enum LaunchRole { ROLE_MAIN = 0, ROLE_REDUCE = 1 };
 
@@ -101,6 +101,7 @@ struct mtk_plan {
   mtk_gemm_desc gemm{};
   mtk_attn_desc attn{};
   mtk_conv_desc conv{};
+  mtk_permute_desc perm{};
   std::vector<Launch> launches;
   size_t workspace = 0;
   bool serial_split = false;          // GEMM split-K run in-workgroup (C written by the main kernel)
@@ -439,6 +440,47 @@ int plan_attn_bwd(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   return MTK_OK;
 }
 
+// OIDHW -> DHWIO weight re-layout: a tiled transpose of src viewed as [O][C*T] (one workgroup per
+// 64 x 64 tile); 16-byte accesses when C*T and O are multiples of 8 (alignment checked at run).
+int plan_permute(mtk_ctx *ctx, const mtk_permute_desc *d_in, mtk_plan **out) {
+  if (!d_in || !out) return fail(MTK_ERR_INVALID, "null descriptor or output");
+  const mtk_permute_desc d = *d_in;
+  if (d.O <= 0 || d.C <= 0 || d.KD <= 0 || d.KH <= 0 || d.KW <= 0)
+    return fail(MTK_ERR_INVALID, "O, C, KD, KH, KW must be positive");
+  const long long T = (long long)d.KD * d.KH * d.KW, CT = T * d.C;
+  const uint64_t bytes = (uint64_t)d.O * CT * 2;
+  if (bytes > kMaxOperandBytes || CT >= (1ll << 31))
+    return fail(MTK_ERR_UNSUPPORTED, "operands above 2 GiB are not supported by this build");
+  mtk_plan *p = new mtk_plan();
+  p->ctx = ctx;
+  p->kind = PLAN_PERMUTE;
+  p->perm = d;
+  const bool vec = CT % 8 == 0 && d.O % 8 == 0;
+  p->align_a = p->align_b = vec ? 16 : 2;
+  Launch g;
+  g.name = vec ? "mtk_permute_oidhw_dhwio_v8" : "mtk_permute_oidhw_dhwio_v1";
+  g.grid = (unsigned)(((d.O + 63) / 64) * ((CT + 63) / 64));
+  mtk_permute_args a{};
+  a.O = d.O;
+  a.C = d.C;
+  a.T = (int)T;
+  set_args(g, a);
+  p->launches.push_back(g);
+  p->flops = 0;
+  p->bytes = 2.0 * (double)bytes;
+  char desc[160];
+  snprintf(desc, sizeof desc, "permute OIDHW->DHWIO O=%d C=%d KD=%d KH=%d KW=%d %s grid=%u", d.O, d.C, d.KD, d.KH, d.KW,
+           vec ? "16-byte" : "2-byte", g.grid);
+  p->description = desc;
+  int s = resolve(p);
+  if (s != MTK_OK) {
+    delete p;
+    return s;
+  }
+  *out = p;
+  return MTK_OK;
+}
+
 // ------------------------------------------------------------------ conv planning
 
 int conv_out(const mtk_conv_desc *d, int *od, int *oh, int *ow) {
@@ -700,6 +742,17 @@ int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
     a.bias = c->bias;
     a.C = c->y;
     a.partial = nullptr;
+  } else if (p->kind == PLAN_PERMUTE) {
+    const mtk_permute_run_args *t = (const mtk_permute_run_args *)argset;
+    if (!t || !t->src || !t->dst) return fail(MTK_ERR_INVALID, "src and dst must be non-null");
+    if (!aligned(t->src, p->align_a) || !aligned(t->dst, p->align_b))
+      return fail(MTK_ERR_INVALID, "src and dst must be %u-byte aligned for this plan", p->align_a);
+    const size_t n = (size_t)p->perm.O * p->perm.C * p->perm.KD * p->perm.KH * p->perm.KW * 2;
+    const char *s0 = (const char *)t->src, *d0 = (const char *)t->dst;
+    if (s0 < d0 + n && d0 < s0 + n) return fail(MTK_ERR_INVALID, "src and dst overlap");
+    mtk_permute_args &a = args_of<mtk_permute_args>(ls[0]);
+    a.src = t->src;
+    a.dst = t->dst;
   } else if (p->kind == PLAN_ATTN_BWD) {
     const mtk_attn_bwd_args *t = (const mtk_attn_bwd_args *)argset;
     if (!t || !t->Q || !t->K || !t->V || !t->O || !t->dO || !t->lse || !t->dQ || !t->dK || !t->dV)
@@ -746,6 +799,8 @@ size_t argset_size(const mtk_plan *p) {
       return sizeof(mtk_conv_args);
     case PLAN_ATTN_BWD:
       return sizeof(mtk_attn_bwd_args);
+    case PLAN_PERMUTE:
+      return sizeof(mtk_permute_run_args);
     default:
       return sizeof(mtk_attn_args);
   }
@@ -983,6 +1038,14 @@ int mtk_attn_bwd_plan(mtk_ctx *ctx, const mtk_attn_desc *desc, mtk_plan **out) {
 }
 int mtk_attn_bwd_run(const mtk_plan *plan, const mtk_attn_bwd_args *args) {
   if (plan && plan->kind != PLAN_ATTN_BWD) return fail(MTK_ERR_INVALID, "not an attention backward plan");
+  return run_plan(plan, args);
+}
+
+int mtk_permute_plan(mtk_ctx *ctx, const mtk_permute_desc *desc, mtk_plan **out) {
+  return plan_permute(ctx, desc, out);
+}
+int mtk_permute_run(const mtk_plan *plan, const mtk_permute_run_args *args) {
+  if (plan && plan->kind != PLAN_PERMUTE) return fail(MTK_ERR_INVALID, "not a permutation plan");
   return run_plan(plan, args);
 }
 

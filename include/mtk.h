@@ -244,6 +244,23 @@ typedef struct {
 /* Replaces TensorOpSession*.run / runWithoutOutputReadback -> execute (ConvolutionShared.swift:922-965). */
 int mtk_conv_run(const mtk_plan *plan, const mtk_conv_args *args);
 
+/* Convolution weight re-layout OIDHW -> DHWIO: replaces permute_oidhw_to_dhwio and
+ * WeightPermutationSession3D (Sources/ConvolutionShared/ConvolutionShared.swift:4593-4629,
+ * 1577-1674): dst[kd][kh][kw][c][o] = src[o][c][kd][kh][kw], 16-bit elements (f16 or bf16 bits),
+ * so PyTorch-style OIDHW (or OIHW with KD = 1) weights can feed mtk_conv_run. Exact copy. */
+typedef struct {
+  int O, C, KD, KH, KW;
+} mtk_permute_desc;
+
+int mtk_permute_plan(mtk_ctx *ctx, const mtk_permute_desc *desc, mtk_plan **out);
+
+typedef struct {
+  const void *src; /* [O][C][KD][KH][KW] */
+  void *dst;       /* [KD][KH][KW][C][O], must not overlap src */
+} mtk_permute_run_args;
+
+int mtk_permute_run(const mtk_plan *plan, const mtk_permute_run_args *args);
+
 /* ------------------------------------------------------------------ plans, validate, profile */
 
 size_t mtk_plan_workspace_bytes(const mtk_plan *plan);
@@ -258,7 +275,8 @@ int mtk_plan_destroy(mtk_plan *plan);
  * gpuStartTime/gpuEndTime measurement (ConvolutionShared.swift:237-247, 2522-2539; matmul.swift:480-489).
  * Runs `warmup` untimed iterations, then `iters` timed ones, cycling through `nsets` argument sets
  * (so a large operand can be rotated to defeat the 256 MB Infinity Cache). Each set is the op's
- * args struct (mtk_gemm_args / mtk_attn_args / mtk_attn_bwd_args / mtk_conv_args). HIP events on the plan's stream
+ * args struct (mtk_gemm_args / mtk_attn_args / mtk_attn_bwd_args / mtk_conv_args /
+ * mtk_permute_run_args). HIP events on the plan's stream
  * bracket each kernel; results are averages per iteration, in milliseconds. */
 typedef struct {
   double total_ms;      /* per iteration, first launch start to last launch end */

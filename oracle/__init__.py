@@ -114,6 +114,7 @@ def lib():
                                          ctypes.c_size_t]
         L.oracle_gemm.argtypes = [ctypes.c_int] * 5 + [u16p, u16p, u16p, f32p] + [ctypes.c_int] * 3
         L.oracle_attention.argtypes = [ctypes.c_int] * 7 + [u16p, u16p, u16p, f32p] + [ctypes.c_int] * 3
+        L.oracle_permute_oidhw_to_dhwio.argtypes = [u16p, u16p] + [ctypes.c_int] * 5
         L.oracle_attention_bwd.argtypes = ([ctypes.c_int] * 7 + [u16p, u16p, u16p, u16p, f32p, f32p, f32p, f32p]
                                            + [ctypes.c_int] * 3)
         L.oracle_conv_out_d.argtypes = [ctypes.POINTER(ConvDims)]
@@ -234,6 +235,15 @@ def attention_bwd(Q, K, V, dO, *, causal=False, dtype="f16", pairs=None, threads
     lib().oracle_attention_bwd(_dt(dtype), B, H, Sq, Skv, D, 1 if causal else 0, pq, pk, pv, pg, _f32p(dQ),
                                _f32p(dK), _f32p(dV), _f32p(Dt), p0, p1, threads)
     return dQ, dK, dV, Dt
+
+
+def permute_oidhw_to_dhwio(w) -> np.ndarray:
+    """[O][C][KD][KH][KW] 16-bit weights -> [KD][KH][KW][C][O] (ConvolutionShared.swift:4606-4627)."""
+    src, ps = _u16(w)
+    O, C, KD, KH, KW = src.shape
+    out = np.empty((KD, KH, KW, C, O), np.uint16)
+    lib().oracle_permute_oidhw_to_dhwio(ps, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), O, C, KD, KH, KW)
+    return out.view(w.dtype) if np.asarray(w).dtype == np.float16 else out
 
 
 def conv(dims: ConvDims, x, w, bias=None, *, rows=None, threads=0) -> np.ndarray:

@@ -410,3 +410,22 @@ void oracle_conv(const oracle_conv_dims *d, const uint16_t *x, const uint16_t *w
   }
   free(wf);
 }
+
+void oracle_permute_oidhw_to_dhwio(const uint16_t *src, uint16_t *dst, int O, int C, int KD, int KH, int KW) {
+  /* ConvolutionShared.swift:4606-4627: destination index gid decomposed as (kd, kh, kw, ic, oc) with
+   * oc fastest; source index ((((oc * C + ic) * KD + kd) * KH + kh) * KW) + kw. */
+  const size_t count = (size_t)O * C * KD * KH * KW;
+  for (size_t gid = 0; gid < count; ++gid) {
+    size_t linear = gid;
+    const size_t oc = linear % (size_t)O;
+    linear /= (size_t)O;
+    const size_t ic = linear % (size_t)C;
+    linear /= (size_t)C;
+    const size_t kw = linear % (size_t)KW;
+    linear /= (size_t)KW;
+    const size_t kh = linear % (size_t)KH;
+    linear /= (size_t)KH;
+    const size_t kd = linear;
+    dst[gid] = src[((((oc * C + ic) * KD + kd) * KH + kh) * KW) + kw];
+  }
+}

@@ -14,6 +14,7 @@
  *   conv2d    Sources/ConvolutionShared/ConvolutionShared.swift:4994-5026
  *   conv3d    Sources/ConvolutionShared/ConvolutionShared.swift:5028-5068
  *   conv+bias Sources/ConvolutionShared/ConvolutionShared.swift:5070-5096
+ *   weight re-layout  Sources/ConvolutionShared/ConvolutionShared.swift:4606-4627 (OIDHW -> DHWIO)
  *   padded    Sources/convolution2d_padding/convolution2d_padding.swift:79-107,
  *             Sources/convolution3d_padding/convolution3d_padding.swift:202-242
  *
@@ -87,6 +88,10 @@ int oracle_conv_out_w(const oracle_conv_dims *d);
  * row_end < 0 means all rows. bias may be NULL. */
 void oracle_conv(const oracle_conv_dims *d, const uint16_t *x, const uint16_t *w, const uint16_t *bias, float *y,
                  long row_begin, long row_end, int nthreads);
+
+/* ---- weight re-layout: dst[((kd*KH + kh)*KW + kw)*C + c)*O + o] = src[(((o*C + c)*KD + kd)*KH + kh)*KW + kw],
+ * 16-bit elements, destination visited in order as the reference's kernel does. */
+void oracle_permute_oidhw_to_dhwio(const uint16_t *src, uint16_t *dst, int O, int C, int KD, int KH, int KW);
 
 #ifdef __cplusplus
 }

@@ -427,3 +427,26 @@ def test_conv3d_depth_padding_and_strides_random(orc):
     # A kernel that is not symmetric must not equal its flip (catches a flipped/convolution kernel).
     yf = orc.conv(dims, x, np.ascontiguousarray(w[::-1, ::-1, ::-1]), b)
     assert not np.allclose(yf, ref, atol=1e-2)
+
+
+# ---------------------------------------------------------------- weight re-layout
+
+@pytest.mark.parametrize("shape", [(1, 1, 1, 1, 1), (5, 3, 1, 3, 3), (8, 4, 3, 3, 3), (3, 7, 2, 5, 4)])
+def test_permute_oidhw_to_dhwio_exact(orc, shape):
+    # ConvolutionShared.swift:4606-4627 restated; pinned by an independent numpy transpose and by the
+    # reference's own check (validateFlatOutput, tolerance 0: exact, 5381-5406)
+    w = orc.normal(130, shape)
+    got = orc.permute_oidhw_to_dhwio(w)
+    ref = np.transpose(w, (2, 3, 4, 1, 0))
+    assert got.shape == ref.shape and np.array_equal(got.view(np.uint16), np.ascontiguousarray(ref).view(np.uint16))
+    # a permutation: every source element appears exactly once
+    assert np.array_equal(np.sort(got.view(np.uint16).ravel()), np.sort(w.view(np.uint16).ravel()))
+
+
+def test_permute_then_conv_equals_dhwio_conv(orc):
+    # the reference's PermuteThenTensorOpSession3D path: OIDHW weights re-laid out, then the DHWIO conv
+    d = orc.ConvDims.conv3d(N=1, D=4, H=5, W=6, C=3, O=4, PF=1, PBk=1, PT=1, PB=1, PL=1, PR=1)
+    x = gen.conv3d_activation(d)
+    w_dhwio = gen.conv3d_weights(d)
+    w_oidhw = np.ascontiguousarray(np.transpose(w_dhwio, (4, 3, 0, 1, 2)))
+    assert np.array_equal(orc.conv(d, x, orc.permute_oidhw_to_dhwio(w_oidhw)), orc.conv(d, x, w_dhwio))
