@@ -21,7 +21,8 @@ accumulation, OpenMP over rows) timed on this host on a bounded row sample of th
 
 ``configs``: every other BASELINE configuration measured the same way (split-K 1 variant of
 config 2, the bf16 decode GEMM in GB/s, conv2d / conv3d, flash attention fwd both masks), plus the
-attention backward at the config 5 shape.
+attention backward at the config 5 shape, attention forward and backward with 8 grouped K/V heads
+at that shape, and the OIDHW -> DHWIO convolution-weight re-layout (GB/s).
 """
 from __future__ import annotations
 
@@ -260,6 +261,15 @@ def main():
                                   dev.upload(inputs.uniform(9 + 100 * c, (desc.O,), -1, 1)), y) for c in range(3)]
                 tm = time_steps(dev, pc, sets_c, args.warmup, steps)
                 cfgs[key] = summarize(pc.describe().split(" kernels:")[0], pc, tm, "mfma", key=key)
+            # OIDHW -> DHWIO weight re-layout at the reference's profile shape (512 x 512, 3x3x3;
+            # AGENTS.md:51), HBM-bound: three rotating source copies
+            pp = mtk.PermutePlan(dev, 512, 512, 3, 3, 3)
+            wsh = (512, 512, 3, 3, 3)
+            dst = dev.empty(int(np.prod(wsh)) * 2)
+            sets_p = [pp.args(dev.upload(inputs.normal(14 + 100 * c, wsh)), dst) for c in range(3)]
+            tm = time_steps(dev, pp, sets_p, args.warmup, steps * 4)
+            cfgs["conv_weight_permute"] = summarize("OIDHW -> DHWIO weight re-layout, O = C = 512, 3x3x3 (f16)", pp, tm,
+                                                    "hbm")
             for causal in (False, True):
                 pa = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
                 shp = (2, 4096, 32, 128)
@@ -288,6 +298,29 @@ def main():
                 cfgs["config5_attn_bwd_causal" if causal else "config5_attn_bwd"] = summarize(
                     f"config 5 shape, flash-attn backward (dQ, dK, dV) {'causal' if causal else 'non-causal'}", pb, tm,
                     "mfma", key="config5_bwd_causal" if causal else "config5_bwd")
+            # grouped K/V heads at the config 5 shape (the reference's Hq / Hk; here Hq = 32, Hk = 8):
+            # forward and backward, non-causal
+            pg = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, H_kv=8)
+            pgb = mtk.AttentionBwdPlan(dev, 2, 32, 4096, 4096, 128, H_kv=8)
+            kvs = (2, 4096, 8, 128)
+            sets_g, sets_gb = [], []
+            ws_g = dev.empty(pgb.workspace_bytes)
+            grads = [dev.empty(int(np.prod(s_)) * 2) for s_ in (shp, kvs, kvs)]
+            for c in range(2):
+                q_c, k_c, v_c = (dev.upload(inputs.normal(20 + i + 100 * c, s_)) for i, s_ in enumerate((shp, kvs, kvs)))
+                o_c, lse_c = dev.empty(int(np.prod(shp)) * 2), dev.empty(2 * 32 * 4096 * 4)
+                sets_g.append(pg.args(q_c, k_c, v_c, o_c, lse_c))
+                pg.run(q_c, k_c, v_c, o_c, lse_c)
+                sets_gb.append(pgb.args(q_c, k_c, v_c, o_c, dev.upload(inputs.normal(23 + 100 * c, shp)), lse_c,
+                                        *grads, ws_g))
+            dev.sync()
+            tm = time_steps(dev, pg, sets_g, args.warmup, steps)
+            cfgs["config5_attn_gqa8"] = summarize("config 5 shape with 8 K/V heads (H=32, H_kv=8), flash-attn fwd",
+                                                  pg, tm, "mfma", key="config5_gqa8")
+            tm = time_steps(dev, pgb, sets_gb, args.warmup, steps)
+            cfgs["config5_attn_bwd_gqa8"] = summarize(
+                "config 5 shape with 8 K/V heads (H=32, H_kv=8), flash-attn backward", pgb, tm, "mfma",
+                key="config5_bwd_gqa8")
         except Exception as e:  # report what was measured; the headline stands on its own
             cfgs["error"] = repr(e)
         line["configs"] = cfgs

@@ -82,7 +82,7 @@ class GemmArgs(ctypes.Structure):
 
 
 class AttnDesc(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_int) for n in ("B", "H", "S_q", "S_kv", "D", "causal", "dtype", "q_rows")]
+    _fields_ = [(n, ctypes.c_int) for n in ("B", "H", "S_q", "S_kv", "D", "causal", "dtype", "q_rows", "H_kv")]
 
 
 class AttnArgs(ctypes.Structure):
@@ -401,14 +401,16 @@ class GemmPlan(_Plan):
 
 
 class AttentionPlan(_Plan):
-    """O = softmax(Q K^T / sqrt(D)) V per (batch, head); tensors [B][S][H][D], D = 128."""
+    """O = softmax(Q K^T / sqrt(D)) V per (batch, head); Q, O [B][S_q][H][D], K, V [B][S_kv][H_kv][D]
+    (H_kv = 0: H; query head h reads K/V head h // (H // H_kv)), D = 128."""
 
     _args_type = AttnArgs
     _run_fn = "mtk_attn_run"
 
-    def __init__(self, device: Device | None, B, H, S_q, S_kv, D=128, *, causal=False, dtype="f16", q_rows=0):
+    def __init__(self, device: Device | None, B, H, S_q, S_kv, D=128, *, causal=False, dtype="f16", q_rows=0,
+                 H_kv=0):
         self.desc = AttnDesc(B=B, H=H, S_q=S_q, S_kv=S_kv, D=D, causal=1 if causal else 0, dtype=_DT[dtype],
-                             q_rows=q_rows)
+                             q_rows=q_rows, H_kv=H_kv)
         h = ctypes.c_void_p()
         _check(lib().mtk_attn_plan(device.handle if device else None, ctypes.byref(self.desc), ctypes.byref(h)))
         super().__init__(h)
@@ -423,13 +425,15 @@ class AttentionPlan(_Plan):
 
 class AttentionBwdPlan(_Plan):
     """dQ, dK, dV of the loss sum(dO * O) (Network.swift:313-402) from Q, K, V, the forward's O and
-    lse, and dO; tensors [B][S][H][D], lse [B][H][S_q] fp32; needs a workspace (the D vector)."""
+    lse, and dO; tensors [B][S][H][D] (K, V, dK, dV with H_kv heads), lse [B][H][S_q] fp32; needs a
+    workspace (the D vector)."""
 
     _args_type = AttnBwdArgs
     _run_fn = "mtk_attn_bwd_run"
 
-    def __init__(self, device: Device | None, B, H, S_q, S_kv, D=128, *, causal=False, dtype="f16"):
-        self.desc = AttnDesc(B=B, H=H, S_q=S_q, S_kv=S_kv, D=D, causal=1 if causal else 0, dtype=_DT[dtype], q_rows=0)
+    def __init__(self, device: Device | None, B, H, S_q, S_kv, D=128, *, causal=False, dtype="f16", H_kv=0):
+        self.desc = AttnDesc(B=B, H=H, S_q=S_q, S_kv=S_kv, D=D, causal=1 if causal else 0, dtype=_DT[dtype], q_rows=0,
+                             H_kv=H_kv)
         h = ctypes.c_void_p()
         _check(lib().mtk_attn_bwd_plan(device.handle if device else None, ctypes.byref(self.desc), ctypes.byref(h)))
         super().__init__(h)
@@ -546,11 +550,11 @@ def gemm(dev: Device, A, B, bias=None, *, trans_b=True, dtype="f16", split_k=1, 
 
 
 def attention(dev: Device, Q, K, V, *, causal=False, dtype="f16", q_rows=0, return_lse=False):
-    """attention.run equivalent on [B][S][H][D] tensors; with return_lse, also the [B][H][S_q]
-    fp32 row log-sum-exp the backward takes."""
+    """attention.run equivalent on [B][S][H][D] tensors (K and V may have fewer heads, dividing H);
+    with return_lse, also the [B][H][S_q] fp32 row log-sum-exp the backward takes."""
     Q, K, V = _bits(Q), _bits(K), _bits(V)
     B, Sq, H, D = Q.shape
-    plan = AttentionPlan(dev, B, H, Sq, K.shape[1], D, causal=causal, dtype=dtype, q_rows=q_rows)
+    plan = AttentionPlan(dev, B, H, Sq, K.shape[1], D, causal=causal, dtype=dtype, q_rows=q_rows, H_kv=K.shape[2])
     dQ, dK, dV = dev.upload(Q), dev.upload(K), dev.upload(V)
     dO = dev.empty(Q.nbytes)
     dl = dev.empty(B * H * Sq * 4) if return_lse else None
@@ -568,7 +572,7 @@ def attention_bwd(dev: Device, Q, K, V, O, dO, lse, *, causal=False, dtype="f16"
     """(dQ, dK, dV) of the loss sum(dO * O) given the forward's O and lse (Network.swift:313-402)."""
     Q, K, V, O, dO = _bits(Q), _bits(K), _bits(V), _bits(O), _bits(dO)
     B, Sq, H, D = Q.shape
-    plan = AttentionBwdPlan(dev, B, H, Sq, K.shape[1], D, causal=causal, dtype=dtype)
+    plan = AttentionBwdPlan(dev, B, H, Sq, K.shape[1], D, causal=causal, dtype=dtype, H_kv=K.shape[2])
     bufs = [dev.upload(x) for x in (Q, K, V, O, dO, np.ascontiguousarray(lse, np.float32))]
     outs = [dev.empty(x.nbytes) for x in (Q, K, V)]
     ws = dev.empty(plan.workspace_bytes)

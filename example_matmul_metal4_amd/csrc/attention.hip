@@ -3,7 +3,9 @@
 // Replaces the reference's generated `attention` kernel (Sources/attention/attention.swift:133-380):
 // O = softmax(Q K^T / sqrt(D)) V with base-2 online softmax (its dotScale = log2(e)/sqrt(D),
 // attention.swift:24), per (batch, head), tensors laid out [B][S][H][D] (attention.swift:466-468
-// with a batch dimension). Extensions: batch, causal mask (keys j <= i + S_kv - S_q), bf16.
+// with a batch dimension). Extensions: batch, causal mask (keys j <= i + S_kv - S_q), bf16, and
+// grouped K/V heads: K, V are [B][S_kv][H_kv][D] and query head h reads K/V head h / (H / H_kv)
+// (the reference declares Hk but indexes K/V with the query head, attention.swift:155-156).
 //
 // Work decomposition
 //   * Workgroup = 4 wavefronts = 128 query rows of one (batch, head); each wave owns 32 queries,
@@ -75,9 +77,11 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
   if (CAUSAL) qb = a.q_blocks - 1 - qb;  // heaviest query blocks first
   const int b = bh / a.H, h = bh - b * a.H;
   const int q0 = qb * kBQ;
-  const uint32_t rs = (uint32_t)a.H * kD * 2;  // bytes between sequence positions
+  const uint32_t rs = (uint32_t)a.H * kD * 2;      // bytes between sequence positions of Q / O
+  const uint32_t rkv = (uint32_t)a.H_kv * kD * 2;  // ... of K / V ([B][S_kv][H_kv][D])
+  const int hk = h / (a.H / a.H_kv);               // the key/value head this query head reads
   const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kD * 2);
-  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H + h) * kD * 2);
+  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H_kv + hk) * kD * 2);
   const rsrc_t rq = make_rsrc(a.Q, a.q_bytes);
   const rsrc_t rk = make_rsrc(a.K, a.kv_bytes);
   const rsrc_t rv = make_rsrc(a.V, a.kv_bytes);
@@ -104,22 +108,22 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
     const int pc = lane & 15;
     kcol[i] = 16u * (uint32_t)(pc ^ (srow[i] & 15));
     vcol[i] = 16u * (uint32_t)(pc ^ (4 * (srow[i] & 3)));
-    klane[i] = (uint32_t)srow[i] * rs + kcol[i];
-    vlane[i] = (uint32_t)srow[i] * rs + vcol[i];
+    klane[i] = (uint32_t)srow[i] * rkv + kcol[i];
+    vlane[i] = (uint32_t)srow[i] * rkv + vcol[i];
   }
   // A tile inside S_kv goes out with its base as the uniform scalar offset (no per-row work); the
   // tile crossing S_kv is loaded row-checked, rows past S_kv reading zero.
   auto issue = [&](const rsrc_t &r, char *dst, const uint32_t (&lane_off)[4], const uint32_t (&col)[4], int t) {
     const int key0 = t * kBKV;
     if (key0 + kBKV <= a.S_kv) {
-      const uint32_t tb = kvbase + (uint32_t)key0 * rs;
+      const uint32_t tb = kvbase + (uint32_t)key0 * rkv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) lds_direct16_s(r, dst + i * 1024, lane_off[i], tb);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = key0 + srow[i];
-        lds_direct16(r, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + col[i] : kOOB);
+        lds_direct16(r, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rkv + col[i] : kOOB);
       }
     }
   };
@@ -322,8 +326,10 @@ __device__ __forceinline__ void attn_fwd_pp(const mtk_attn_kargs &a) {
   const int b = bh / a.H, h = bh - b * a.H;
   const int q0 = qb * kBQP;
   const uint32_t rs = (uint32_t)a.H * kD * 2;
+  const uint32_t rkv = (uint32_t)a.H_kv * kD * 2;
+  const int hk = h / (a.H / a.H_kv);
   const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kD * 2);
-  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H + h) * kD * 2);
+  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H_kv + hk) * kD * 2);
   const rsrc_t rq = make_rsrc(a.Q, a.q_bytes);
   const rsrc_t rk = make_rsrc(a.K, a.kv_bytes);
   const rsrc_t rv = make_rsrc(a.V, a.kv_bytes);
@@ -351,20 +357,20 @@ __device__ __forceinline__ void attn_fwd_pp(const mtk_attn_kargs &a) {
   uint32_t klane[2], vlane[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    klane[i] = (uint32_t)stage_row(i) * rs + stage_col(i, true);
-    vlane[i] = (uint32_t)stage_row(i) * rs + stage_col(i, false);
+    klane[i] = (uint32_t)stage_row(i) * rkv + stage_col(i, true);
+    vlane[i] = (uint32_t)stage_row(i) * rkv + stage_col(i, false);
   }
   auto issue = [&](const rsrc_t &r, char *dst, const uint32_t (&lane_off)[2], bool is_k, int t) {
     const int key0 = t * kBKV;
     if (key0 + kBKV <= a.S_kv) {
-      const uint32_t tb = kvbase + (uint32_t)key0 * rs;
+      const uint32_t tb = kvbase + (uint32_t)key0 * rkv;
 #pragma unroll
       for (int i = 0; i < 2; ++i) lds_direct16_s(r, dst + i * 1024, lane_off[i], tb);
     } else {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int key = key0 + stage_row(i);
-        lds_direct16(r, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rs + stage_col(i, is_k) : kOOB);
+        lds_direct16(r, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rkv + stage_col(i, is_k) : kOOB);
       }
     }
   };

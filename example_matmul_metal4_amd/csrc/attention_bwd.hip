@@ -10,10 +10,13 @@
 //   dV = P^T dO,  dK = dS^T Q,  dQ = dS K
 // Three kernels, no atomics (every output element is written once, sums in a fixed order):
 //   attn_bwd_pre   D for every query row.
-//   attn_bwd_dkdv  one workgroup per 128 keys of one (batch, head), 4 wavefronts x 32 keys; the
-//                  query rows stream through LDS in tiles of 64. S = Q.K^T is computed with the
-//                  key as the accumulator column, Q rows fed in the order swap_bits_2_3(m) so that
-//                  accumulator registers 0-7 / 8-15 hold 8 consecutive queries: P and dS leave the
+//   attn_bwd_dkdv  one workgroup per 128 keys of one (batch, K/V head), 4 wavefronts x 32 keys; the
+//                  query rows of every query head sharing that K/V head stream through LDS in tiles
+//                  of 64 (grouped-query attention: H query heads over H_kv K/V heads, query head h
+//                  reads K/V head h / (H / H_kv); dK and dV sum over the group). S = Q.K^T is
+//                  computed with the key as the accumulator column, Q rows fed in the order
+//                  swap_bits_2_3(m) so that accumulator registers 0-7 / 8-15 hold 8 consecutive
+//                  queries: P and dS leave the
 //                  accumulators as the B operands of dV^T += dO^T.P and dK^T += Q^T.dS, whose
 //                  A operands are transposed LDS reads (ds_read_b64_tr_b16) of the dO / Q tiles.
 //   attn_bwd_dq    one workgroup per 256 queries, 8 wavefronts x 32 queries (the forward's shape):
@@ -117,13 +120,13 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   const int g = lane >> 5, col = lane & 31;
 
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = id / a.k_blocks;
+  const int bh = id / a.k_blocks;  // (batch, K/V head)
   const int kb = id - bh * a.k_blocks;
-  const int b = bh / a.H, h = bh - b * a.H;
+  const int b = bh / a.H_kv, hk = bh - b * a.H_kv;
+  const int group = a.H / a.H_kv;  // query heads hk * group .. hk * group + group - 1
   const int k0 = kb * kBwdKeys;
-  const uint32_t rs = (uint32_t)a.H * kBD * 2;
-  const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kBD * 2);
-  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H + h) * kBD * 2);
+  const uint32_t rs = (uint32_t)a.H * kBD * 2, rkv = (uint32_t)a.H_kv * kBD * 2;
+  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H_kv + hk) * kBD * 2);
   const rsrc_t rq = make_rsrc(a.Q, a.q_bytes);
   const rsrc_t rg = make_rsrc(a.dO, a.q_bytes);
   const rsrc_t rk = make_rsrc(a.K, a.kv_bytes);
@@ -131,7 +134,6 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   const uint32_t row_bytes = (uint32_t)a.B * a.H * a.S_q * 4u;  // lse and D: [B][H][S_q] fp32
   const rsrc_t rl = make_rsrc(a.lse, row_bytes);
   const rsrc_t rd = make_rsrc(a.Dt, row_bytes);
-  const uint32_t row_base = (uint32_t)(((size_t)b * a.H + h) * a.S_q) * 4u;
   const int diag = a.S_kv - a.S_q;  // key j is visible to query i iff j <= i + diag (causal)
   const float c = a.scale_log2;
 
@@ -141,19 +143,26 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   u32x4 kf[8], vf[8];
 #pragma unroll
   for (int ds = 0; ds < 8; ++ds) {
-    const uint32_t off = key_ok ? kvbase + (uint32_t)key * rs + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB;
+    const uint32_t off = key_ok ? kvbase + (uint32_t)key * rkv + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB;
     kf[ds] = buf_load16(rk, off);
     vf[ds] = buf_load16(rv, off);
   }
 
-  // query tiles that see at least one of this workgroup's keys
+  // query tiles that see at least one of this workgroup's keys: t0 .. n_tiles - 1 of each query
+  // head of the group, visited head by head (step i: head hk * group + i / per_head, tile
+  // t0 + i % per_head)
   int t0 = 0;
   if (CAUSAL) t0 = max(0, k0 - diag) / kBwdQTile;
   const int n_tiles = (a.S_q + kBwdQTile - 1) / kBwdQTile;
+  const int per_head = max(0, n_tiles - t0);
+  const int n_steps = group * per_head;
 
-  auto stage = [&](int slot, int t) {
+  auto stage = [&](int slot, int i) {
     char *st = smem + slot * kStageBytes;
+    const int h = hk * group + i / per_head, t = t0 + i % per_head;
     const int valid = a.S_q - t * kBwdQTile;
+    const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kBD * 2);
+    const uint32_t row_base = (uint32_t)(((size_t)b * a.H + h) * a.S_q) * 4u;
     const uint32_t tb = qbase + (uint32_t)(t * kBwdQTile) * rs;
     stage_rows<4, false>(rq, st, 16 * wave, tb, rs, valid, lane);
     stage_rows<4, true>(rq, st + kRowTile, 16 * wave, tb, rs, valid, lane);
@@ -176,15 +185,15 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     dv[i] = f32x16{};
   }
 
-  if (t0 < n_tiles) stage(t0 & 1, t0);
-  for (int t = t0; t < n_tiles; ++t) {
+  if (n_steps > 0) stage(0, 0);
+  for (int i = 0; i < n_steps; ++i) {
     wait_vmem();
-    __syncthreads();  // tile t is in LDS; everyone is done with tile t-1's slot
-    if (t + 1 < n_tiles) stage((t + 1) & 1, t + 1);
-    const char *st = smem + (t & 1) * kStageBytes;
+    __syncthreads();  // step i's tile is in LDS; everyone is done with step i-1's slot
+    if (i + 1 < n_steps) stage((i + 1) & 1, i + 1);
+    const char *st = smem + (i & 1) * kStageBytes;
     const char *qrow = st, *qtr = st + kRowTile, *grow = st + 2 * kRowTile, *gtr = st + 3 * kRowTile;
     const float *lse_t = (const float *)(st + 4 * kRowTile), *d_t = (const float *)(st + 4 * kRowTile + 1024);
-    const int qt0 = t * kBwdQTile;
+    const int qt0 = (t0 + i % per_head) * kBwdQTile;
 
     // S and dP for the two 32-query blocks of the tile
     f32x16 s[2], p[2];
@@ -263,7 +272,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   if (key_ok) {
     uint16_t *dK = (uint16_t *)a.dK;
     uint16_t *dV = (uint16_t *)a.dV;
-    const size_t base = (((size_t)b * a.S_kv + key) * a.H + h) * kBD;
+    const size_t base = (((size_t)b * a.S_kv + key) * a.H_kv + hk) * kBD;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -293,10 +302,11 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
   int qblk = id - bh * a.q_blocks;
   if (CAUSAL) qblk = a.q_blocks - 1 - qblk;  // heaviest query blocks first
   const int b = bh / a.H, h = bh - b * a.H;
+  const int hk = h / (a.H / a.H_kv);  // K/V head of query head h
   const int q0 = qblk * kBwdQRows;
-  const uint32_t rs = (uint32_t)a.H * kBD * 2;
+  const uint32_t rs = (uint32_t)a.H * kBD * 2, rkv = (uint32_t)a.H_kv * kBD * 2;
   const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kBD * 2);
-  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H + h) * kBD * 2);
+  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H_kv + hk) * kBD * 2);
   const rsrc_t rq = make_rsrc(a.Q, a.q_bytes);
   const rsrc_t rg = make_rsrc(a.dO, a.q_bytes);
   const rsrc_t rk = make_rsrc(a.K, a.kv_bytes);
@@ -325,10 +335,10 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
   auto stage = [&](int slot, int t) {
     char *st = smem + slot * 3 * kRowTile;
     const int valid = a.S_kv - t * kBwdKTile;
-    const uint32_t tb = kvbase + (uint32_t)(t * kBwdKTile) * rs;
-    stage_rows<2, false>(rk, st, 8 * wave, tb, rs, valid, lane);
-    stage_rows<2, true>(rk, st + kRowTile, 8 * wave, tb, rs, valid, lane);
-    stage_rows<2, false>(rv, st + 2 * kRowTile, 8 * wave, tb, rs, valid, lane);
+    const uint32_t tb = kvbase + (uint32_t)(t * kBwdKTile) * rkv;
+    stage_rows<2, false>(rk, st, 8 * wave, tb, rkv, valid, lane);
+    stage_rows<2, true>(rk, st + kRowTile, 8 * wave, tb, rkv, valid, lane);
+    stage_rows<2, false>(rv, st + 2 * kRowTile, 8 * wave, tb, rkv, valid, lane);
   };
 
   const int arow = bwd_swap_bits_2_3(col);  // MFMA row m reads key swap_bits_2_3(m) of the block

@@ -9,7 +9,7 @@
 
 #include <stdint.h>
 
-#define MTK_KARGS_VERSION 6
+#define MTK_KARGS_VERSION 7
 
 /* Tile-GEMM kernels: plain GEMM (A [M][K] . B, B either [N][K] or [K][N]) and
  * implicit-GEMM convolution (A = im2col of an NDHWC activation, B = DHWIO
@@ -88,6 +88,7 @@ typedef struct {
   float scale_log2; /* log2(e) / sqrt(D) */
   uint32_t q_bytes, kv_bytes;
   float *lse; /* [B][H][S_q] natural-log row log-sum-exp of the scaled scores, or NULL */
+  int32_t H_kv; /* K/V heads (divides H): query head h reads K/V head h / (H / H_kv) */
 } mtk_attn_kargs;
 
 /* Flash-attention backward (all three kernels of the plan take this block). */
@@ -97,6 +98,7 @@ typedef struct {
   float *Dt;        /* [B][H][S_q] workspace: rowsum(dO * O) */
   void *dQ, *dK, *dV;
   int32_t B, H, S_q, S_kv;
+  int32_t H_kv;     /* K/V heads (divides H); dK, dV sum over the H / H_kv query heads of a group */
   int32_t q_blocks; /* ceil(S_q / 256): dQ workgroups per (batch, head) */
   int32_t k_blocks; /* ceil(S_kv / 128): dK/dV workgroups per (batch, head) */
   int32_t causal;

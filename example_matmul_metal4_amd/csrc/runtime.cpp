@@ -376,11 +376,14 @@ int plan_attn_bwd(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   if (!d_in || !out) return fail(MTK_ERR_INVALID, "null descriptor or output");
   mtk_attn_desc d = *d_in;
   if (d.B <= 0 || d.H <= 0 || d.S_q <= 0 || d.S_kv <= 0) return fail(MTK_ERR_INVALID, "B, H, S_q, S_kv must be positive");
+  if (d.H_kv == 0) d.H_kv = d.H;
+  if (d.H_kv < 0 || d.H % d.H_kv != 0)
+    return fail(MTK_ERR_INVALID, "H_kv must divide H (got H=%d, H_kv=%d)", d.H, d.H_kv);
   if (d.D != 128) return fail(MTK_ERR_UNSUPPORTED, "head dimension must be 128 (got %d)", d.D);
   if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "attention dtype must be MTK_F16 or MTK_BF16");
   if (d.q_rows != 0) return fail(MTK_ERR_INVALID, "the backward plan chooses its own blocking (q_rows must be 0)");
   const uint64_t q_bytes = (uint64_t)d.B * d.S_q * d.H * d.D * 2;
-  const uint64_t kv_bytes = (uint64_t)d.B * d.S_kv * d.H * d.D * 2;
+  const uint64_t kv_bytes = (uint64_t)d.B * d.S_kv * d.H_kv * d.D * 2;
   if (q_bytes > kMaxOperandBytes || kv_bytes > kMaxOperandBytes)
     return fail(MTK_ERR_UNSUPPORTED, "operands above 2 GiB are not supported by this build");
   mtk_plan *p = new mtk_plan();
@@ -393,6 +396,7 @@ int plan_attn_bwd(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   mtk_attn_bwd_kargs a{};
   a.B = d.B;
   a.H = d.H;
+  a.H_kv = d.H_kv;
   a.S_q = d.S_q;
   a.S_kv = d.S_kv;
   a.q_blocks = (d.S_q + 255) / 256;
@@ -406,7 +410,7 @@ int plan_attn_bwd(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   pre.name = std::string("mtk_attn_bwd_pre_") + dt;
   pre.grid = (unsigned)(((long long)d.B * d.S_q * d.H + 15) / 16);
   kv.name = std::string("mtk_attn_bwd_dkdv_") + dt + cz;
-  kv.grid = (unsigned)((long long)a.k_blocks * d.B * d.H);
+  kv.grid = (unsigned)((long long)a.k_blocks * d.B * d.H_kv);  // per K/V head: sums over its query heads
   q.name = std::string("mtk_attn_bwd_dq_") + dt + cz;
   q.grid = (unsigned)((long long)a.q_blocks * d.B * d.H);
   q.block = 512;
@@ -428,8 +432,8 @@ int plan_attn_bwd(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   p->flops = 10.0 * d.B * d.H * d.D * pairs;
   p->bytes = 4.0 * (double)q_bytes + 4.0 * (double)kv_bytes + 3.0 * 4.0 * d.B * d.H * d.S_q;
   char desc[256];
-  snprintf(desc, sizeof desc, "attention bwd %s B=%d H=%d S_q=%d S_kv=%d D=%d causal=%d grids=%u/%u/%u", dt, d.B,
-           d.H, d.S_q, d.S_kv, d.D, d.causal, pre.grid, kv.grid, q.grid);
+  snprintf(desc, sizeof desc, "attention bwd %s B=%d H=%d H_kv=%d S_q=%d S_kv=%d D=%d causal=%d grids=%u/%u/%u", dt,
+           d.B, d.H, d.H_kv, d.S_q, d.S_kv, d.D, d.causal, pre.grid, kv.grid, q.grid);
   p->description = desc;
   int s = resolve(p);
   if (s != MTK_OK) {
@@ -630,12 +634,15 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   if (!d_in || !out) return fail(MTK_ERR_INVALID, "null descriptor or output");
   mtk_attn_desc d = *d_in;
   if (d.B <= 0 || d.H <= 0 || d.S_q <= 0 || d.S_kv <= 0) return fail(MTK_ERR_INVALID, "B, H, S_q, S_kv must be positive");
+  if (d.H_kv == 0) d.H_kv = d.H;
+  if (d.H_kv < 0 || d.H % d.H_kv != 0)
+    return fail(MTK_ERR_INVALID, "H_kv must divide H (got H=%d, H_kv=%d)", d.H, d.H_kv);
   if (d.D != 128) return fail(MTK_ERR_UNSUPPORTED, "head dimension must be 128 (got %d)", d.D);
   if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "attention dtype must be MTK_F16 or MTK_BF16");
   if (d.q_rows != 0 && d.q_rows != 128 && d.q_rows != 256)
     return fail(MTK_ERR_INVALID, "q_rows must be 0, 128 or 256 (got %d)", d.q_rows);
   const uint64_t q_bytes = (uint64_t)d.B * d.S_q * d.H * d.D * 2;
-  const uint64_t kv_bytes = (uint64_t)d.B * d.S_kv * d.H * d.D * 2;
+  const uint64_t kv_bytes = (uint64_t)d.B * d.S_kv * d.H_kv * d.D * 2;
   if (q_bytes > kMaxOperandBytes || kv_bytes > kMaxOperandBytes)
     return fail(MTK_ERR_UNSUPPORTED, "operands above 2 GiB are not supported by this build");
   mtk_plan *p = new mtk_plan();
@@ -659,6 +666,7 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   mtk_attn_kargs a{};
   a.B = d.B;
   a.H = d.H;
+  a.H_kv = d.H_kv;
   a.S_q = d.S_q;
   a.S_kv = d.S_kv;
   a.q_blocks = (d.S_q + rows - 1) / rows;
@@ -680,8 +688,8 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   p->flops = 4.0 * d.B * d.H * d.D * pairs;
   p->bytes = 2.0 * (double)q_bytes + 2.0 * (double)kv_bytes;
   char desc[256];
-  snprintf(desc, sizeof desc, "attention fwd %s B=%d H=%d S_q=%d S_kv=%d D=%d causal=%d rows/wg=%d grid=%u",
-           d.dtype == MTK_F16 ? "f16" : "bf16", d.B, d.H, d.S_q, d.S_kv, d.D, d.causal, rows, g.grid);
+  snprintf(desc, sizeof desc, "attention fwd %s B=%d H=%d H_kv=%d S_q=%d S_kv=%d D=%d causal=%d rows/wg=%d grid=%u",
+           d.dtype == MTK_F16 ? "f16" : "bf16", d.B, d.H, d.H_kv, d.S_q, d.S_kv, d.D, d.causal, rows, g.grid);
   p->description = desc;
   int s = resolve(p);
   if (s != MTK_OK) {

@@ -157,8 +157,12 @@ int mtk_gemm_run(const mtk_plan *plan, const mtk_gemm_args *args);
 
 /* Replaces BlockDimenions / AttentionDimensions{R, C, K, Hq, Hk} and the R,C,Hq,Hk function
  * constants (Sources/attention/attention.swift:9-21, 117-120, 423-431).
- * Q, O: [B][S_q][H][D]; K, V: [B][S_kv][H][D] (the reference's [S][H][D] packing,
+ * Q, O: [B][S_q][H][D]; K, V: [B][S_kv][H_kv][D] (the reference's [S][H][D] packing,
  * attention.swift:466-468, with a batch dimension). D must be 128. scale = 1/sqrt(D).
+ * H_kv (appended; 0 = H) is the reference's Hk: H must be a multiple of it and query head h reads
+ * K/V head h / (H / H_kv) (grouped-query attention). The reference declares Hk (attention.swift:20,
+ * 131) but slices K and V at the query head (attention.swift:156), so it defines only Hq == Hk,
+ * where both mappings agree.
  * causal != 0 keeps keys j <= i + (S_kv - S_q) for query i (bottom-right aligned).
  * q_rows: query rows per workgroup, 0 = let the plan choose; 128 (4 wavefronts of 32 queries, two
  * workgroups per CU) or 256 (8 wavefronts of 32 queries in two groups that alternate MFMA and
@@ -168,6 +172,7 @@ typedef struct {
   int causal;
   int dtype;  /* MTK_F16 (MTK_BF16 accepted) */
   int q_rows; /* appended: earlier fields keep their offsets */
+  int H_kv;   /* appended: K/V heads, 0 = H */
 } mtk_attn_desc;
 
 /* Replaces createSource(blockDimensions:attentionDimensions:buildOptions:) + pipeline setup
@@ -193,8 +198,9 @@ int mtk_attn_run(const mtk_plan *plan, const mtk_attn_args *args);
  * (derivativeQ / derivativeK / derivativeV) and has no GPU kernel for:
  *   P = exp(Q K^T / sqrt(D) - lse), D_i = sum_d dO_id O_id, dS = P (dO V^T - D) / sqrt(D),
  *   dV = P^T dO, dK = dS^T Q, dQ = dS K.
- * Same descriptor as the forward (q_rows must be 0); same layouts; causal as in the forward. The
- * plan needs a workspace of mtk_plan_workspace_bytes (the D vector). Deterministic: no atomics. */
+ * Same descriptor as the forward (q_rows must be 0); same layouts; causal as in the forward. With
+ * H_kv < H, dK and dV of a K/V head sum the contributions of its H / H_kv query heads. The plan
+ * needs a workspace of mtk_plan_workspace_bytes (the D vector). Deterministic: no atomics. */
 int mtk_attn_bwd_plan(mtk_ctx *ctx, const mtk_attn_desc *desc, mtk_plan **out);
 
 typedef struct {

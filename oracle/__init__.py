@@ -113,9 +113,9 @@ def lib():
         L.oracle_fill_normal.argtypes = [ctypes.c_uint64, ctypes.c_double, ctypes.c_double, ctypes.c_int, u16p,
                                          ctypes.c_size_t]
         L.oracle_gemm.argtypes = [ctypes.c_int] * 5 + [u16p, u16p, u16p, f32p] + [ctypes.c_int] * 3
-        L.oracle_attention.argtypes = [ctypes.c_int] * 7 + [u16p, u16p, u16p, f32p] + [ctypes.c_int] * 3
+        L.oracle_attention.argtypes = [ctypes.c_int] * 8 + [u16p, u16p, u16p, f32p] + [ctypes.c_int] * 3
         L.oracle_permute_oidhw_to_dhwio.argtypes = [u16p, u16p] + [ctypes.c_int] * 5
-        L.oracle_attention_bwd.argtypes = ([ctypes.c_int] * 7 + [u16p, u16p, u16p, u16p, f32p, f32p, f32p, f32p]
+        L.oracle_attention_bwd.argtypes = ([ctypes.c_int] * 8 + [u16p, u16p, u16p, u16p, f32p, f32p, f32p, f32p]
                                            + [ctypes.c_int] * 3)
         L.oracle_conv_out_d.argtypes = [ctypes.POINTER(ConvDims)]
         L.oracle_conv.argtypes = [ctypes.POINTER(ConvDims), u16p, u16p, u16p, f32p, ctypes.c_long, ctypes.c_long,
@@ -199,40 +199,42 @@ def gemm(A, B, bias=None, *, trans_b=True, dtype="f16", rows=None, threads=0) ->
 
 
 def attention(Q, K, V, *, causal=False, dtype="f16", rows=None, threads=0) -> np.ndarray:
-    """fp32 O for Q,K,V laid out [B][S][H][D] (Network.swift:134-179, 286-311).
+    """fp32 O for Q,K,V laid out [B][S][H][D] (Network.swift:134-179, 286-311). K and V may have
+    fewer heads H_kv dividing H: query head h reads K/V head h // (H // H_kv).
 
     ``rows=(q0, q1)`` computes only those query rows of every (b, h)."""
     q, pq = _u16(Q)
     k, pk = _u16(K)
     v, pv = _u16(V)
     B, Sq, H, D = q.shape
-    Skv = k.shape[1]
-    assert k.shape == (B, Skv, H, D) and v.shape == k.shape
+    Skv, Hkv = k.shape[1], k.shape[2]
+    assert k.shape == (B, Skv, Hkv, D) and v.shape == k.shape and H % Hkv == 0
     O = np.zeros((B, Sq, H, D), np.float32)
     q0, q1 = rows if rows is not None else (0, Sq)
-    lib().oracle_attention(_dt(dtype), B, H, Sq, Skv, D, 1 if causal else 0, pq, pk, pv, _f32p(O), q0, q1, threads)
+    lib().oracle_attention(_dt(dtype), B, H, Hkv, Sq, Skv, D, 1 if causal else 0, pq, pk, pv, _f32p(O), q0, q1, threads)
     return O
 
 
 def attention_bwd(Q, K, V, dO, *, causal=False, dtype="f16", pairs=None, threads=0):
     """fp32 (dQ, dK, dV, Dterm) of the reference's loss sum(dO * O) for Q, K, V, dO laid out
-    [B][S][H][D] (Network.swift:205-281, 313-402); Dterm is [B][H][S_q].
+    [B][S][H][D] (Network.swift:205-281, 313-402); Dterm is [B][H][S_q]. K and V may have fewer
+    heads H_kv (grouped as in ``attention``); dK and dV then sum over each group's query heads.
 
-    ``pairs=(p0, p1)`` computes only the (b, h) pairs with flat index b*H + h in [p0, p1); the
-    other slices of the outputs stay zero."""
+    ``pairs=(p0, p1)`` computes only the (b, hk) pairs with flat index b*H_kv + hk in [p0, p1) (with
+    every query head of the group); the other slices of the outputs stay zero."""
     q, pq = _u16(Q)
     k, pk = _u16(K)
     v, pv = _u16(V)
     g, pg = _u16(dO)
     B, Sq, H, D = q.shape
-    Skv = k.shape[1]
-    assert k.shape == (B, Skv, H, D) and v.shape == k.shape and g.shape == q.shape
+    Skv, Hkv = k.shape[1], k.shape[2]
+    assert k.shape == (B, Skv, Hkv, D) and v.shape == k.shape and g.shape == q.shape and H % Hkv == 0
     dQ = np.zeros((B, Sq, H, D), np.float32)
-    dK = np.zeros((B, Skv, H, D), np.float32)
-    dV = np.zeros((B, Skv, H, D), np.float32)
+    dK = np.zeros((B, Skv, Hkv, D), np.float32)
+    dV = np.zeros((B, Skv, Hkv, D), np.float32)
     Dt = np.zeros((B, H, Sq), np.float32)
     p0, p1 = pairs if pairs is not None else (0, -1)
-    lib().oracle_attention_bwd(_dt(dtype), B, H, Sq, Skv, D, 1 if causal else 0, pq, pk, pv, pg, _f32p(dQ),
+    lib().oracle_attention_bwd(_dt(dtype), B, H, Hkv, Sq, Skv, D, 1 if causal else 0, pq, pk, pv, pg, _f32p(dQ),
                                _f32p(dK), _f32p(dV), _f32p(Dt), p0, p1, threads)
     return dQ, dK, dV, Dt
 

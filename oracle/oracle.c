@@ -166,15 +166,18 @@ void oracle_gemm(int dtype, int M, int N, int K, int trans_b, const uint16_t *A,
 
 /* ------------------------------------------------------------------ attention */
 
-void oracle_attention(int dtype, int B, int H, int S_q, int S_kv, int D, int causal, const uint16_t *Q,
+void oracle_attention(int dtype, int B, int H, int Hkv, int S_q, int S_kv, int D, int causal, const uint16_t *Q,
                       const uint16_t *K, const uint16_t *V, float *O, int q_begin, int q_end, int nthreads) {
-  /* Network.swift:134-179 (S row, scale, max, exp-sum, lse, P) and 286-311 (O = P.V), per (b, h, row). */
+  /* Network.swift:134-179 (S row, scale, max, exp-sum, lse, P) and 286-311 (O = P.V), per (b, h, row).
+   * Query head h reads K/V head h / (H / Hkv). */
   if (q_begin < 0) q_begin = 0;
   if (q_end > S_q || q_end < 0) q_end = S_q;
   const int rows = q_end - q_begin;
   const long total = (long)B * H * rows;
   const float scale = 1.0f / sqrtf((float)D);
   const size_t ldq = (size_t)H * D; /* [B][S][H][D]: consecutive sequence positions are H*D apart */
+  const size_t ldkv = (size_t)Hkv * D;
+  const int group = H / Hkv;
   int nt = pick_threads(nthreads);
 #pragma omp parallel num_threads(nt)
   {
@@ -187,8 +190,8 @@ void oracle_attention(int dtype, int B, int H, int S_q, int S_kv, int D, int cau
       const int h = (int)((t / rows) % H);
       const int i = q_begin + (int)(t % rows);
       const uint16_t *qp = Q + ((size_t)b * S_q + i) * ldq + (size_t)h * D;
-      const uint16_t *kb = K + (size_t)b * S_kv * ldq + (size_t)h * D;
-      const uint16_t *vb = V + (size_t)b * S_kv * ldq + (size_t)h * D;
+      const uint16_t *kb = K + (size_t)b * S_kv * ldkv + (size_t)(h / group) * D;
+      const uint16_t *vb = V + (size_t)b * S_kv * ldkv + (size_t)(h / group) * D;
       float *op = O + ((size_t)b * S_q + i) * ldq + (size_t)h * D;
       int ncols = S_kv;
       if (causal) {
@@ -199,7 +202,7 @@ void oracle_attention(int dtype, int B, int H, int S_q, int S_kv, int D, int cau
       for (int d = 0; d < D; ++d) o[d] = 0.0f;
       if (ncols > 0) {
         for (int j = 0; j < ncols; ++j) { /* createMatrixSRow */
-          const uint16_t *kp = kb + (size_t)j * ldq;
+          const uint16_t *kp = kb + (size_t)j * ldkv;
           float dot = 0.0f;
           for (int d = 0; d < D; ++d) dot += q[d] * to_f32(dtype, kp[d]);
           srow[j] = dot;
@@ -214,7 +217,7 @@ void oracle_attention(int dtype, int B, int H, int S_q, int S_kv, int D, int cau
         const float lse = maximum + logf(sum);
         for (int j = 0; j < ncols; ++j) srow[j] = expf(scale * srow[j] - lse);
         for (int j = 0; j < ncols; ++j) { /* O[d] = sum_j P[j] * V[j][d], j ascending per d */
-          const uint16_t *vp = vb + (size_t)j * ldq;
+          const uint16_t *vp = vb + (size_t)j * ldkv;
           const float p = srow[j];
           for (int d = 0; d < D; ++d) o[d] += p * to_f32(dtype, vp[d]);
         }
@@ -229,18 +232,21 @@ void oracle_attention(int dtype, int B, int H, int S_q, int S_kv, int D, int cau
 
 /* ------------------------------------------------------------------ convolution */
 
-void oracle_attention_bwd(int dtype, int B, int H, int S_q, int S_kv, int D, int causal, const uint16_t *Q,
+void oracle_attention_bwd(int dtype, int B, int H, int Hkv, int S_q, int S_kv, int D, int causal, const uint16_t *Q,
                           const uint16_t *K, const uint16_t *V, const uint16_t *dO, float *dQ, float *dK, float *dV,
                           float *Dterm, int bh_begin, int bh_end, int nthreads) {
   /* Per (b, h), rows i ascending (Network.swift): P row (createMatrixPRow, 151-179), O row = P.V and
    * D = O . dO (createDerivativeSRow 221-238), dP row = dO.V^T (205-218), dS = P (dP - D) * scale
    * (240-251); dQ row = dS.K, columns ascending per d (derivativeQ 376-401); dV[j] += P_j dO[i] and
    * dK[j] += dS_j Q[i], accumulated over rows in order (derivativeV 319-338, derivativeK 341-360).
-   * One thread owns one (b, h), so every sum keeps the reference's order. */
+   * One thread owns one (b, K/V head): its query heads h = hk * group + 0 .. group - 1 in order, each
+   * with rows ascending, so every sum keeps the reference's order (with Hkv == H, one (b, h)).
+   * [bh_begin, bh_end) ranges over the B * Hkv (batch, K/V head) pairs. */
   if (bh_begin < 0) bh_begin = 0;
-  if (bh_end < 0 || bh_end > B * H) bh_end = B * H;
+  if (bh_end < 0 || bh_end > B * Hkv) bh_end = B * Hkv;
   const float scale = 1.0f / sqrtf((float)D);
-  const size_t ldq = (size_t)H * D;
+  const size_t ldq = (size_t)H * D, ldkv = (size_t)Hkv * D;
+  const int group = H / Hkv;
   int nt = pick_threads(nthreads);
   if (nt > bh_end - bh_begin) nt = bh_end - bh_begin > 0 ? bh_end - bh_begin : 1;
 #pragma omp parallel num_threads(nt)
@@ -257,16 +263,17 @@ void oracle_attention_bwd(int dtype, int B, int H, int S_q, int S_kv, int D, int
     float *dv = (float *)malloc(sizeof(float) * (size_t)S_kv * D + 1);
 #pragma omp for schedule(dynamic, 1)
     for (int bh = bh_begin; bh < bh_end; ++bh) {
-      const int b = bh / H, h = bh % H;
-      const uint16_t *kb = K + (size_t)b * S_kv * ldq + (size_t)h * D;
-      const uint16_t *vb = V + (size_t)b * S_kv * ldq + (size_t)h * D;
+      const int b = bh / Hkv, hk = bh % Hkv;
+      const uint16_t *kb = K + (size_t)b * S_kv * ldkv + (size_t)hk * D;
+      const uint16_t *vb = V + (size_t)b * S_kv * ldkv + (size_t)hk * D;
       for (int j = 0; j < S_kv; ++j)
         for (int d = 0; d < D; ++d) {
-          kf[(size_t)j * D + d] = to_f32(dtype, kb[(size_t)j * ldq + d]);
-          vf[(size_t)j * D + d] = to_f32(dtype, vb[(size_t)j * ldq + d]);
+          kf[(size_t)j * D + d] = to_f32(dtype, kb[(size_t)j * ldkv + d]);
+          vf[(size_t)j * D + d] = to_f32(dtype, vb[(size_t)j * ldkv + d]);
         }
       memset(dk, 0, sizeof(float) * (size_t)S_kv * D);
       memset(dv, 0, sizeof(float) * (size_t)S_kv * D);
+      for (int h = hk * group; h < hk * group + group; ++h)
       for (int i = 0; i < S_q; ++i) {
         const uint16_t *qp = Q + ((size_t)b * S_q + i) * ldq + (size_t)h * D;
         const uint16_t *gp = dO + ((size_t)b * S_q + i) * ldq + (size_t)h * D;
@@ -328,8 +335,8 @@ void oracle_attention_bwd(int dtype, int B, int H, int S_q, int S_kv, int D, int
         for (int d = 0; d < D; ++d) dqp[d] = dq[d];
       }
       for (int j = 0; j < S_kv; ++j) {
-        float *dkp = dK + ((size_t)b * S_kv + j) * ldq + (size_t)h * D;
-        float *dvp = dV + ((size_t)b * S_kv + j) * ldq + (size_t)h * D;
+        float *dkp = dK + ((size_t)b * S_kv + j) * ldkv + (size_t)hk * D;
+        float *dvp = dV + ((size_t)b * S_kv + j) * ldkv + (size_t)hk * D;
         for (int d = 0; d < D; ++d) {
           dkp[d] = dk[(size_t)j * D + d];
           dvp[d] = dv[(size_t)j * D + d];

@@ -56,18 +56,20 @@ void oracle_fill_normal(uint64_t seed, double mean, double stddev, int dtype, ui
 void oracle_gemm(int dtype, int M, int N, int K, int trans_b, const uint16_t *A, const uint16_t *B,
                  const uint16_t *bias, float *C, int row_begin, int row_end, int nthreads);
 
-/* ---- attention forward, layout [B][S][H][D] for Q/K/V/O.
+/* ---- attention forward, layout [B][S][H][D] for Q/O, [B][S][Hkv][D] for K/V (query head h reads
+ * K/V head h / (H / Hkv); Hkv divides H).
  * Query rows [q_begin, q_end) of every (b, h) are written (O is full size).
  * causal != 0 keeps keys j <= i + (S_kv - S_q). */
-void oracle_attention(int dtype, int B, int H, int S_q, int S_kv, int D, int causal, const uint16_t *Q,
+void oracle_attention(int dtype, int B, int H, int Hkv, int S_q, int S_kv, int D, int causal, const uint16_t *Q,
                       const uint16_t *K, const uint16_t *V, float *O, int q_begin, int q_end, int nthreads);
 
 /* ---- attention backward (gradients of the reference's loss Phi = sum dO * O), layout
- * [B][S][H][D] for Q/K/V/dO and for the fp32 outputs dQ/dK/dV. The (b, h) pairs with flat index
- * b*H + h in [bh_begin, bh_end) are computed (bh_end < 0: all); their slices of dQ/dK/dV are
- * overwritten, other slices are left alone. Dterm ([B][H][S_q] fp32, the row sums
- * dO . O with O = P.V in fp32) may be NULL. causal != 0 as in oracle_attention. */
-void oracle_attention_bwd(int dtype, int B, int H, int S_q, int S_kv, int D, int causal, const uint16_t *Q,
+ * [B][S][H][D] for Q/dO/dQ and [B][S][Hkv][D] for K/V/dK/dV (fp32 outputs); heads grouped as in
+ * oracle_attention, dK/dV summing over the group's query heads. The (b, hk) pairs with flat index
+ * b*Hkv + hk in [bh_begin, bh_end) are computed (bh_end < 0: all), each with all its query heads;
+ * their slices of dQ/dK/dV are overwritten, other slices are left alone. Dterm ([B][H][S_q] fp32,
+ * the row sums dO . O with O = P.V in fp32) may be NULL. causal != 0 as in oracle_attention. */
+void oracle_attention_bwd(int dtype, int B, int H, int Hkv, int S_q, int S_kv, int D, int causal, const uint16_t *Q,
                           const uint16_t *K, const uint16_t *V, const uint16_t *dO, float *dQ, float *dK, float *dV,
                           float *Dterm, int bh_begin, int bh_end, int nthreads);
 

@@ -265,6 +265,22 @@ def test_attention_select_and_validation():
     assert e.value.status == mtk.MTK_ERR_INVALID
 
 
+def test_attention_grouped_kv_heads_plan():
+    # H_kv (the reference's Hk) defaults to H; must divide H; the dK/dV grid runs per K/V head
+    assert "H=8 H_kv=8 " in mtk.AttentionPlan(None, 1, 8, 512, 512, 128).describe()
+    p = mtk.AttentionPlan(None, 1, 8, 512, 512, 128, H_kv=2)
+    assert "H=8 H_kv=2 " in p.describe() and "rows/wg=128 grid=32" in p.describe()  # per query head
+    assert p.work()[0] == mtk.AttentionPlan(None, 1, 8, 512, 512, 128).work()[0]
+    b = mtk.AttentionBwdPlan(None, 2, 8, 512, 300, 128, H_kv=2)
+    assert "grids=512/12/32" in b.describe()  # pre: 2*512*8/16, dkdv: 3 key blocks * 2 * 2, dq: 2 * 2 * 8
+    assert b.workspace_bytes == 2 * 8 * 512 * 4
+    for hkv in (3, -1, 16):
+        for plan in (mtk.AttentionPlan, mtk.AttentionBwdPlan):
+            with pytest.raises(mtk.MtkError) as e:
+                plan(None, 1, 8, 64, 64, 128, H_kv=hkv)
+            assert e.value.status == mtk.MTK_ERR_INVALID
+
+
 def test_validate_helper_matches_numpy():
     rng = np.random.default_rng(0)
     e = rng.standard_normal(1000).astype(np.float32)

@@ -62,18 +62,29 @@ def _check(name, got, exp, bound_terms, dtype):
     assert worst <= 1.0, (name, worst)
 
 
-def _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=90, pairs=None):
+def _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=90, pairs=None, Hkv=None):
     D = 128
-    print(f"[attn bwd] B={B} H={H} S_q={Sq} S_kv={Skv} causal={causal} {dtype} pairs={pairs}", flush=True)
+    Hkv = Hkv or H
+    group = H // Hkv
+    print(f"[attn bwd] B={B} H={H} H_kv={Hkv} S_q={Sq} S_kv={Skv} causal={causal} {dtype} pairs={pairs}", flush=True)
     Q = oracle.normal(seed, (B, Sq, H, D), dtype=dtype)
-    K = oracle.normal(seed + 1, (B, Skv, H, D), dtype=dtype)
-    V = oracle.normal(seed + 2, (B, Skv, H, D), dtype=dtype)
+    K = oracle.normal(seed + 1, (B, Skv, Hkv, D), dtype=dtype)
+    V = oracle.normal(seed + 2, (B, Skv, Hkv, D), dtype=dtype)
     G = oracle.normal(seed + 3, (B, Sq, H, D), dtype=dtype)
     O, lse = mtk.attention(dev, Q, K, V, causal=causal, dtype=dtype, return_lse=True)
     dQ, dK, dV = mtk.attention_bwd(dev, Q, K, V, O, G, lse, causal=causal, dtype=dtype)
     eQ, eK, eV, _ = oracle.attention_bwd(Q, K, V, G, causal=causal, dtype=dtype, pairs=pairs)
+    if group > 1:
+        # dQ is what full multi-head attention on K/V repeated over each group gives, bit for bit
+        Ke, Ve = np.repeat(K, group, 2), np.repeat(V, group, 2)
+        Oe, lse_e = mtk.attention(dev, Q, Ke, Ve, causal=causal, dtype=dtype, return_lse=True)
+        assert np.array_equal(Oe.view(np.uint16), O.view(np.uint16)) and np.array_equal(lse_e, lse)
+        fQ, _, _ = mtk.attention_bwd(dev, Q, Ke, Ve, Oe, G, lse_e, causal=causal, dtype=dtype)
+        assert np.array_equal(fQ.view(np.uint16), dQ.view(np.uint16))
+        K, V = Ke, Ve  # magnitudes per query head; the dK/dV terms are summed over the group below
     sel = slice(None)
     if pairs is not None:  # compare the computed (b, h) pairs only; Q/K/V magnitudes restricted to them
+        assert group == 1
         bh = [(p // H, p % H) for p in range(*pairs)]
         sub = lambda x: np.stack([x[b, :, h] for b, h in bh])[:, :, None]  # [n][S][1][D]
         Q, K, V, G = sub(Q), sub(K), sub(V), sub(G)
@@ -82,8 +93,9 @@ def _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=90, pairs=None):
     s = 1.0 / np.sqrt(D)
     q, k, g = (np.abs(_f64(x, dtype)) for x in (Q, K, G))
     w = ads + s * p * dmag  # [B][H][Sq][Skv]
-    _check("dV", dV[sel], eV, np.einsum("bhij,bihd->bjhd", p, g), dtype)
-    _check("dK", dK[sel], eK, np.einsum("bhij,bihd->bjhd", w, q), dtype)
+    per_group = lambda t: t.reshape(t.shape[0], t.shape[1], -1, group, D).sum(3)  # sum a group's query heads
+    _check("dV", dV[sel], eV, per_group(np.einsum("bhij,bihd->bjhd", p, g)), dtype)
+    _check("dK", dK[sel], eK, per_group(np.einsum("bhij,bihd->bjhd", w, q)), dtype)
     _check("dQ", dQ[sel], eQ, np.einsum("bhij,bjhd->bihd", w, k), dtype)
 
 
@@ -98,6 +110,17 @@ def _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=90, pairs=None):
 ])
 def test_attention_bwd_matches_oracle(dev, B, H, Sq, Skv, causal, dtype):
     _run_and_check(dev, B, H, Sq, Skv, causal, dtype)
+
+
+@pytest.mark.parametrize("B,H,Hkv,Sq,Skv,causal,dtype", [
+    (1, 4, 1, 200, 200, False, "f16"),
+    (2, 8, 2, 130, 300, True, "f16"),
+    (1, 6, 3, 257, 129, True, "bf16"),
+])
+def test_attention_bwd_grouped_kv_heads(dev, B, H, Hkv, Sq, Skv, causal, dtype):
+    # grouped K/V heads (the reference's Hk, attention.swift:20, 120): dK, dV of a K/V head sum over
+    # the query heads that read it
+    _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=70, Hkv=Hkv)
 
 
 @pytest.mark.parametrize("causal", [False, True])

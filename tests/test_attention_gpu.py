@@ -33,6 +33,8 @@ def check(dev, Q, K, V, causal, dtype="f16", label="", q_rows=0):
     print(f"[attn] {label} Q{Q.shape} Skv={K.shape[1]} causal={causal} {dtype} q_rows={q_rows}", flush=True)
     got = mtk.attention(dev, Q, K, V, causal=causal, dtype=dtype, q_rows=q_rows)
     exp = oracle.attention(Q, K, V, causal=causal, dtype=dtype)
+    group = Q.shape[2] // K.shape[2]  # grouped K/V heads: bound terms per query head
+    K, V = np.repeat(K, group, 2), np.repeat(V, group, 2)
     p = probs_f64(Q, K, causal, dtype)
     absv = np.abs(oracle.to_f32(V, dtype).astype(np.float64))
     abspv = np.einsum("bhij,bjhd->bihd", p, absv)
@@ -106,6 +108,20 @@ def test_closed_forms(dev, q_rows):
     assert np.array_equal(O[:, 0], V[:, 0])
     O = mtk.attention(dev, Q, K, V, causal=True, q_rows=q_rows)  # query 256 (second block of 256)
     assert np.array_equal(O, mtk.attention(dev, Q, K, V, causal=True, q_rows=384 - q_rows))  # both kernels: same bits
+
+
+@pytest.mark.parametrize("H,Hkv", [(8, 2), (6, 1), (4, 4)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("q_rows", ROWS)
+def test_grouped_kv_heads(dev, H, Hkv, causal, q_rows):
+    # the reference's Hq / Hk dimensions (attention.swift:20, 120): query head h reads K/V head
+    # h // (H // Hkv); same bits as multi-head attention on K/V repeated over each group
+    B, Sq, Skv = 2, 300, 270
+    Q = oracle.normal(60, (B, Sq, H, 128))
+    K, V = oracle.normal(61, (B, Skv, Hkv, 128)), oracle.normal(62, (B, Skv, Hkv, 128))
+    got, _ = check(dev, Q, K, V, causal, label=f"H{H}/Hkv{Hkv}", q_rows=q_rows)
+    full = mtk.attention(dev, Q, np.repeat(K, H // Hkv, 2), np.repeat(V, H // Hkv, 2), causal=causal, q_rows=q_rows)
+    assert np.array_equal(got.view(np.uint16), full.view(np.uint16))
 
 
 def test_config5_full_size_sampled_rows(dev):

@@ -359,6 +359,32 @@ def test_attention_bwd_key_permutation_equivariance(orc):
         assert not p[0, :, :2].any() and not p[1, :, 1:].any()
 
 
+def test_attention_grouped_kv_heads_equal_repeated_heads(orc):
+    # grouped K/V heads: query head h reads K/V head h // (H // Hkv). Forward and dQ equal multi-head
+    # attention on K/V repeated over each group, bit for bit (same values, same loop order); dK and
+    # dV equal the group sums of the repeated problem's per-head gradients (up to summation order).
+    B, S, H, Hkv, D = 2, 24, 6, 2, 32
+    Q, G = orc.normal(140, (B, S, H, D)), orc.normal(143, (B, S, H, D))
+    K, V = orc.normal(141, (B, S + 5, Hkv, D)), orc.normal(142, (B, S + 5, Hkv, D))
+    Ke, Ve = np.repeat(K, H // Hkv, 2), np.repeat(V, H // Hkv, 2)
+    for causal in (False, True):
+        assert np.array_equal(orc.attention(Q, K, V, causal=causal), orc.attention(Q, Ke, Ve, causal=causal))
+        dQ, dK, dV, Dt = orc.attention_bwd(Q, K, V, G, causal=causal)
+        fQ, fK, fV, fD = orc.attention_bwd(Q, Ke, Ve, G, causal=causal)
+        assert np.array_equal(dQ, fQ) and np.array_equal(Dt, fD)
+        for got, full in ((dK, fK), (dV, fV)):
+            summed = full.reshape(B, S + 5, Hkv, H // Hkv, D).sum(3)
+            assert np.allclose(got, summed, rtol=1e-5, atol=1e-6)
+    # a transposed grouping (h % Hkv) would differ
+    Kt, Vt = np.tile(K, (1, 1, H // Hkv, 1)), np.tile(V, (1, 1, H // Hkv, 1))
+    assert not np.array_equal(orc.attention(Q, K, V), orc.attention(Q, Kt, Vt))
+    # pairs select (b, K/V head) with every query head of the group
+    part = orc.attention_bwd(Q, K, V, G, pairs=(1, 2))  # (b, hk) = (0, 1): query heads 3..5
+    full = orc.attention_bwd(Q, K, V, G)
+    assert np.array_equal(part[0][0, :, 3:], full[0][0, :, 3:]) and not part[0][0, :, :3].any()
+    assert np.array_equal(part[1][0, :, 1], full[1][0, :, 1]) and not part[1][1].any()
+
+
 def test_attention_bwd_fixture_regression(orc, golden_dir):
     fx = np.load(os.path.join(golden_dir, "seeded.npz"))
     for tag, causal in (("", False), ("_causal", True)):
