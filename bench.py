@@ -269,7 +269,7 @@ def main():
             sets_p = [pp.args(dev.upload(inputs.normal(14 + 100 * c, wsh)), dst) for c in range(3)]
             tm = time_steps(dev, pp, sets_p, args.warmup, steps * 4)
             cfgs["conv_weight_permute"] = summarize("OIDHW -> DHWIO weight re-layout, O = C = 512, 3x3x3 (f16)", pp, tm,
-                                                    "hbm")
+                                                    "hbm", key="conv_weight_permute")
             for causal in (False, True):
                 pa = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
                 shp = (2, 4096, 32, 128)

@@ -268,21 +268,37 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     }
   }
 
-  // dK[key][d], dV[key][d]: lane = key, register 4 rq + e of block db = d 32 db + 8 rq + 4 g + e
-  if (key_ok) {
-    uint16_t *dK = (uint16_t *)a.dK;
-    uint16_t *dV = (uint16_t *)a.dV;
-    const size_t base = (((size_t)b * a.S_kv + key) * a.H_kv + hk) * kBD;
+  // dK[key][d], dV[key][d]: lane = key, register 4 rq + e of block db = d 32 db + 8 rq + 4 g + e.
+  // The tiles go through LDS (free after the loop): each wave parks its 32 keys as 256-byte rows
+  // (16-byte chunk c of row r at chunk c ^ (r & 15)), then stores whole rows, 16 bytes per lane, so
+  // every store instruction writes four complete rows instead of 8-byte pieces of 32 rows.
+  __syncthreads();  // every wave is done reading the last stage
+  char *pk = smem + wave * (2 * 32 * 256), *pv = pk + 32 * 256;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d = db * 32 + 8 * rq + 4 * g;
-        *(u32x2 *)(dK + base + d) = u32x2{pack2<DT>(dk[db][4 * rq], dk[db][4 * rq + 1]),
-                                          pack2<DT>(dk[db][4 * rq + 2], dk[db][4 * rq + 3])};
-        *(u32x2 *)(dV + base + d) = u32x2{pack2<DT>(dv[db][4 * rq], dv[db][4 * rq + 1]),
-                                          pack2<DT>(dv[db][4 * rq + 2], dv[db][4 * rq + 3])};
-      }
+    for (int rq = 0; rq < 4; ++rq) {
+      const uint32_t o = (uint32_t)(col * 256 + (((4 * db + rq) ^ (col & 15)) << 4) + 8 * g);
+      *(u32x2 *)(pk + o) = u32x2{pack2<DT>(dk[db][4 * rq], dk[db][4 * rq + 1]),
+                                 pack2<DT>(dk[db][4 * rq + 2], dk[db][4 * rq + 3])};
+      *(u32x2 *)(pv + o) = u32x2{pack2<DT>(dv[db][4 * rq], dv[db][4 * rq + 1]),
+                                 pack2<DT>(dv[db][4 * rq + 2], dv[db][4 * rq + 3])};
+    }
+  __syncthreads();
+  uint16_t *dK = (uint16_t *)a.dK;
+  uint16_t *dV = (uint16_t *)a.dV;
+  const size_t base0 = ((size_t)b * a.S_kv * a.H_kv + hk) * kBD;
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int r = 4 * it + (lane >> 4), pc = lane & 15;
+    const int kr = k0 + wave * 32 + r;
+    const uint32_t o = (uint32_t)(r * 256 + ((pc ^ (r & 15)) << 4));
+    const u32x4 vk = *(const u32x4 *)(pk + o), vv = *(const u32x4 *)(pv + o);
+    if (kr < a.S_kv) {
+      const size_t e = base0 + (size_t)kr * a.H_kv * kBD + 8 * pc;
+      *(u32x4 *)(dK + e) = vk;
+      *(u32x4 *)(dV + e) = vv;
+    }
   }
 }
 

@@ -8,8 +8,11 @@ once; only the plan's kernels run in the loop.
 
 Cases: gemm (config 2, 4096 x 4096 x 4100 + bias, B [N][K]), gemm_nn (4096^3, B [K][N]), decode
 (config 3, bf16 M=16, 3 rotating input copies), conv2d / conv3d (config 4), attn / attn_causal
-(config 5), attn_bwd / attn_bwd_causal (the backward at the config 5 shape), copy (torch's device-to-device copy of 256 MiB: known HBM traffic of 256 MiB read and
-256 MiB written per launch, used to scale the FETCH_SIZE / WRITE_SIZE counters).
+(config 5), attn_bwd / attn_bwd_causal (the backward at the config 5 shape), attn_gqa8 /
+attn_bwd_gqa8 (forward / backward at the config 5 shape with 8 K/V heads), permute (OIDHW -> DHWIO
+weight re-layout, 512 x 512 x 3x3x3, 3 rotating source copies), copy (torch's device-to-device copy
+of 256 MiB: known HBM traffic of 256 MiB read and 256 MiB written per launch, used to scale the
+FETCH_SIZE / WRITE_SIZE counters).
 """
 import argparse
 import sys
@@ -20,7 +23,7 @@ import numpy as np
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("case", choices=["gemm", "gemm_nn", "decode", "conv2d", "conv3d", "attn", "attn_causal", "attn_bwd",
-                                     "attn_bwd_causal", "copy"])
+                                     "attn_bwd_causal", "attn_gqa8", "attn_bwd_gqa8", "permute", "copy"])
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--split", type=int, default=4)
     ap.add_argument("--tile", type=int, default=0)
@@ -83,6 +86,24 @@ def main(argv=None):
             sets = [plan.args(dev.upload(inputs.uniform(7, xs, -1, 1)), dev.upload(inputs.uniform(8, wsh, -1, 1)),
                               dev.upload(inputs.uniform(9, (desc.O,), -1, 1)),
                               dev.empty(int(np.prod(plan.out_shape())) * 2))]
+        elif a.case == "permute":
+            wsh = (512, 512, 3, 3, 3)
+            plan = mtk.PermutePlan(dev, *wsh)
+            dst = dev.empty(int(np.prod(wsh)) * 2)
+            sets = [plan.args(dev.upload(inputs.normal(14 + 100 * c, wsh)), dst) for c in range(3)]
+        elif a.case in ("attn_gqa8", "attn_bwd_gqa8"):
+            shp, kvs = (2, 4096, 32, 128), (2, 4096, 8, 128)
+            fwd = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, H_kv=8)
+            q, k, v = (dev.upload(inputs.normal(20 + i, s_)) for i, s_ in enumerate((shp, kvs, kvs)))
+            o, lse = dev.empty(int(np.prod(shp)) * 2), dev.empty(2 * 32 * 4096 * 4)
+            if a.case == "attn_gqa8":
+                plan, sets = fwd, [fwd.args(q, k, v, o, lse)]
+            else:
+                fwd.run(q, k, v, o, lse)
+                plan = mtk.AttentionBwdPlan(dev, 2, 32, 4096, 4096, 128, H_kv=8)
+                sets = [plan.args(q, k, v, o, dev.upload(inputs.normal(23, shp)), lse,
+                                  *(dev.empty(int(np.prod(s_)) * 2) for s_ in (shp, kvs, kvs)),
+                                  dev.empty(plan.workspace_bytes))]
         elif a.case in ("attn_bwd", "attn_bwd_causal"):
             causal = a.case == "attn_bwd_causal"
             shp = (2, 4096, 32, 128)
