@@ -420,18 +420,24 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
     }
   }
 
-  // dQ[qi][d]: lane = query, register 4 rq + e of block db = d 32 db + 8 rq + 4 g + e
-  if (q_ok) {
-    uint16_t *dQ = (uint16_t *)a.dQ;
-    const size_t base = (((size_t)b * a.S_q + qi) * a.H + h) * kBD;
+  // dQ[qi][d]: lane = query, register 4 rq + e of block db = d 32 db + 8 rq + 4 g + e; parked in
+  // LDS as 256-byte rows and stored as whole rows, as in the dK/dV kernel
+  __syncthreads();  // every wave is done reading the last stage
+  char *pq = smem + wave * (32 * 256);
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d = db * 32 + 8 * rq + 4 * g;
-        *(u32x2 *)(dQ + base + d) = u32x2{pack2<DT>(dq[db][4 * rq], dq[db][4 * rq + 1]),
-                                          pack2<DT>(dq[db][4 * rq + 2], dq[db][4 * rq + 3])};
-      }
+    for (int rq = 0; rq < 4; ++rq)
+      *(u32x2 *)(pq + col * 256 + (((4 * db + rq) ^ (col & 15)) << 4) + 8 * g) =
+          u32x2{pack2<DT>(dq[db][4 * rq], dq[db][4 * rq + 1]), pack2<DT>(dq[db][4 * rq + 2], dq[db][4 * rq + 3])};
+  __syncthreads();
+  uint16_t *dQ = (uint16_t *)a.dQ;
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int r = 4 * it + (lane >> 4), pc = lane & 15;
+    const int qr = q0 + wave * 32 + r;
+    const u32x4 v = *(const u32x4 *)(pq + r * 256 + ((pc ^ (r & 15)) << 4));
+    if (qr < a.S_q) *(u32x4 *)(dQ + (((size_t)b * a.S_q + qr) * a.H + h) * kBD + 8 * pc) = v;
   }
 }
 
