@@ -22,7 +22,8 @@ accumulation, OpenMP over rows) timed on this host on a bounded row sample of th
 ``configs``: every other BASELINE configuration measured the same way (split-K 1 variant of
 config 2, the bf16 decode GEMM in GB/s, conv2d / conv3d, flash attention fwd both masks), plus the
 attention backward at the config 5 shape, attention forward and backward with 8 grouped K/V heads
-at that shape, and the OIDHW -> DHWIO convolution-weight re-layout (GB/s).
+at that shape, the OIDHW -> DHWIO convolution-weight re-layout (GB/s) and the reference's own
+default GEMM run (M=32, N=3072, K=80000, split-K 30; GB/s).
 """
 from __future__ import annotations
 
@@ -244,6 +245,13 @@ def main():
             tm = time_steps(dev, p3, s3, args.warmup, steps * 4)
             cfgs["config3_decode"] = summarize("config 3: bf16 M=16 N=14336 K=4096 split-K 8 + bias (HBM-bound)",
                                                p3, tm, "hbm", key="config3_decode")
+            # the reference's own default run (matmul.swift:334): M=32, N=3072, K=80000, split-K 30;
+            # HBM-bound (B is 491 MB), three rotating input copies
+            p4, s4 = gemm_case(dev, mtk, inputs, 32, 3072, 80000, "f16", 30, (50, 51, 52),
+                               (nrm(1 / np.sqrt(80000)), nrm(1 / np.sqrt(80000)), uni(-0.5, 0.5)))
+            tm = time_steps(dev, p4, s4, args.warmup, steps)
+            cfgs["reference_main_large_k"] = summarize("reference main(): f16 M=32 N=3072 K=80000 split-K 30 + bias",
+                                                       p4, tm, "hbm", key="reference_main_large_k")
             for key, dims in (("config4a_conv2d", dict(rank=2, N=8, D=1, H=128, W=128, C=256, O=256, KD=1, KH=3, KW=3,
                                                        pad_top=1, pad_bottom=1, pad_left=1, pad_right=1)),
                               ("config4b_conv3d", dict(rank=3, N=1, D=16, H=64, W=64, C=128, O=128, KD=3, KH=3, KW=3,

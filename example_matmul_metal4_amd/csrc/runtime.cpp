@@ -259,8 +259,10 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   int tile = d.tile;
   int split = d.split_k;
   if (tile == 0) {
+    // 256x256 tiles when there are enough of them (with the requested split) to fill the device,
+    // unless M or N fits a 128 tile: a 256 tile would then compute mostly padding
     const long long t256 = (long long)((d.M + 255) / 256) * ((d.N + 255) / 256);
-    tile = (t256 * std::max(split, 1) >= 128) ? 256 : 128;
+    tile = (t256 * std::max(split, 1) >= 128 && d.M > 128 && d.N > 128) ? 256 : 128;
   }
   const int tiles_m = (d.M + tile - 1) / tile, tiles_n = (d.N + tile - 1) / tile;
   const long long tiles = (long long)tiles_m * tiles_n;

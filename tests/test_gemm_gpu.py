@@ -292,6 +292,17 @@ def test_run_errors(dev):
     assert "workspace" in e.value.message
 
 
+@pytest.mark.parametrize("tile", [0, 128])
+def test_reference_main_shape_large_k(dev, tile):
+    # the reference's own default run (matmul.swift:334): M=32, N=3072, K=80000, split-K 30;
+    # every output element is checked
+    M, N, K = 32, 3072, 80000
+    A = oracle.normal(50, (M, K), 0, 1 / np.sqrt(K))
+    B = oracle.normal(51, (N, K), 0, 1 / np.sqrt(K))
+    bias = oracle.uniform(52, (N,), -0.5, 0.5)
+    check(dev, A, B, bias, split_k=30, tile=tile, label="reference main()")
+
+
 def test_config3_decode_skinny_full_size(dev):
     # bf16 M=16, N=14336, K=4096, split-K=8, A ~ N(0,1), B ~ N(0,0.02),
     # bias ~ N(0,0.02), fp32 accumulate, bf16 out. Every output element is checked.
