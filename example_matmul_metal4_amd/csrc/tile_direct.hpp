@@ -302,6 +302,12 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   };
   int split_end = SERIAL ? split_first_tile(a, 1, t) : 0;  // SERIAL: first K-tile of the next partition
   int parked = 0;                                           // SERIAL: partitions parked in the workspace
+  // SERIAL: the K-tile after a partition boundary had its next tile's loads issued at the boundary,
+  // ahead of the slot stores; it waits for those loads only (vmcnt(kSlotStores): vector memory
+  // operations complete in issue order, so at most the stores are then outstanding).
+  bool preissued = false;
+  constexpr int kSlotStores = TM * TN * 4;  // slot store instructions per wavefront and boundary
+  static_assert(kSlotStores < 64, "vmcnt range");
   if (kt0 < kt1) issue_all(smem, kt0);
   wait_vmem();
   __syncthreads();
@@ -318,10 +324,10 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   // SERIAL: the K loop runs once per partition (the pipeline carries on across the boundary: the
   // last K-tile of a partition prefetches the next one's first); the partition sum is parked
   // between the runs.
-  int kt = kt0;
-  for (;;) {
-    const int kstop = SERIAL ? min(split_end, kfull) : kfull;
-    for (; kt < kstop; ++kt) {
+  // One K-tile of the pipeline. PRE (SERIAL only): the first K-tile after a partition boundary,
+  // whose next tile's loads went out at the boundary.
+  auto ktile = [&](const int kt, auto pre_c) {
+      constexpr bool PRE = decltype(pre_c)::value;
       const int cur = (kt - kt0) & 1;
       char *nxt = smem + (cur ^ 1) * kStage;
       // The next tile is the partial last K-tile when there is one. Without one, the last iteration
@@ -340,8 +346,15 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
         if (ks == kLast) {
           // the next tile has landed (own loads: vmcnt; everyone's: barrier) and every wave is done
           // reading this tile's stage, which the next iteration starts to overwrite
-          wait_vmem();
-          __syncthreads();
+          if constexpr (PRE) {
+            // the slot stores issued after this tile's loads may still be in flight (raw barrier:
+            // __syncthreads' fence would wait for them)
+            __builtin_amdgcn_s_waitcnt((kSlotStores & 15) | ((kSlotStores >> 4) << 14) | 0x70);  // vmcnt(S) lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+          } else {
+            wait_vmem();
+            __syncthreads();
+          }
         }
         // this k-step's fragments read by inline asm (one k-step earlier)
         if constexpr (AOP::kAsmFrag) lgkm_wait0(fa[c]);
@@ -356,7 +369,9 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
 #pragma unroll
           for (int u = 0; u < kPerGroup; ++u) {
             const int q = (ks * TM + i) * kPerGroup + u;
-            if (q < PA) {
+            if (PRE) {
+              // issued at the partition boundary
+            } else if (q < PA) {
               if constexpr (AOP::kIsConv)
                 opa.issue(ra, nxt, q, tp);
               else
@@ -378,7 +393,16 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
           __builtin_amdgcn_sched_barrier(0);
         }
       }
+  };
+
+  int kt = kt0;
+  for (;;) {
+    const int kstop = SERIAL ? min(split_end, kfull) : kfull;
+    if constexpr (SERIAL) {
+      if (preissued && kt < kstop) ktile(kt++, std::true_type{});
+      preissued = false;
     }
+    for (; kt < kstop; ++kt) ktile(kt, std::false_type{});
     if constexpr (!SERIAL) {
       break;
     } else {
@@ -386,6 +410,10 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       // anywhere else (or at K itself) after the last partition. Only boundaries park, so every
       // slot written is one of this tile's split_k-1.
       if (kt != split_end || split_end >= a.k_tiles || parked >= a.split_k - 1) break;
+      // The loads K-tile kt would issue (tile kt + 1, into the stage of tile kt - 1, which every
+      // wave finished reading before the last barrier) go out now, ahead of the slot traffic.
+      issue_all(smem + ((((kt - kt0) & 1)) ^ 1) * kStage, min(kt + 1, kt1 - 1));
+      preissued = true;
       if (parked == 0) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
