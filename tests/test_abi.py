@@ -172,6 +172,17 @@ def test_gemm_kernel_select_dry():
     assert "split_k=2 k_tiles/split=1" in p.describe()
 
 
+def test_gemm_small_m_large_k_plan():
+    # the reference's default run (matmul.swift:334): M = 32 fits a 128 tile, so the plan takes
+    # 128x128 tiles (24 of them) with the requested 30 partitions of 42 K-tiles, two-pass
+    p = mtk.GemmPlan(None, 32, 3072, 80000, has_bias=True, split_k=30)
+    d = p.describe()
+    assert "tile=128x128 split_k=30 k_tiles/split=42 " in d and "grid=720 " in d
+    assert d.endswith("kernels: mtk_gemm_f16_nt_128x128_d mtk_splitk_reduce_f16")
+    assert p.workspace_bytes == 30 * 32 * 3072 * 4
+    assert "tile=256x256" in mtk.GemmPlan(None, 32, 3072, 80000, split_k=30, tile=256).describe()
+
+
 @pytest.mark.parametrize("kw,status", [
     (dict(M=0, N=4, K=4), mtk.MTK_ERR_INVALID),
     (dict(M=4, N=4, K=-1), mtk.MTK_ERR_INVALID),
