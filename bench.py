@@ -144,6 +144,48 @@ def cpu_baseline(target_s=10.0):
                       f"{threads} threads of {cpu}"}
 
 
+def cpu_baselines_other(target_s=3.0):
+    """The CPU oracle on bounded samples of the other MFMA-bound configs:
+    attention (config 5, Network.swift:134-179 / 286-311 restated) on a block of query rows of
+    every (b, h), conv2d (config 4a, ConvolutionShared.swift:4994-5026) on a block of output rows.
+    Each sample grows until it takes about target_s seconds; TFLOP/s counts the sampled work."""
+    import oracle
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    out = {}
+    Q = oracle.normal(10, (2, 4096, 32, 128))
+    K = oracle.normal(11, (2, 4096, 32, 128))
+    V = oracle.normal(12, (2, 4096, 32, 128))
+    rows = 4
+    while True:
+        t0 = time.perf_counter()
+        oracle.attention(Q, K, V, rows=(0, rows), threads=threads)
+        el = time.perf_counter() - t0
+        if el >= target_s or rows >= 4096:
+            break
+        rows = min(4096, max(rows * 2, int(rows * target_s / max(el, 1e-3)) + 1))
+    out["config5_attn"] = {"value": 4.0 * 2 * 32 * rows * 4096 * 128 / el / 1e12, "unit": "TFLOP/s", "cores": threads,
+                           "kind": "port", "sample": f"oracle_attention on query rows 0..{rows - 1} of every (b, h) "
+                                                     f"of config 5 (non-causal), {el:.2f} s"}
+    dims = oracle.ConvDims.conv2d(N=8, H=128, W=128, C=256, O=256, PT=1, PB=1, PL=1, PR=1)
+    x = oracle.uniform(7, dims.x_shape(), -1, 1)
+    w = oracle.uniform(8, dims.w_shape(), -1, 1)
+    b = oracle.uniform(9, (dims.O,), -1, 1)
+    nrows = 2
+    total = dims.N * dims.OH
+    while True:
+        t0 = time.perf_counter()
+        oracle.conv(dims, x, w, b, rows=(0, nrows), threads=threads)
+        el = time.perf_counter() - t0
+        if el >= target_s or nrows >= total:
+            break
+        nrows = min(total, max(nrows * 2, int(nrows * target_s / max(el, 1e-3)) + 1))
+    out["config4a_conv2d"] = {"value": 2.0 * nrows * dims.OW * dims.O * 9 * dims.C / el / 1e12, "unit": "TFLOP/s",
+                              "cores": threads, "kind": "port",
+                              "sample": f"oracle_conv on output rows 0..{nrows - 1} (of {total}) of config 4a, {el:.2f} s"}
+    return out
+
+
 def traffic_for(key):
     """HBM bytes per launch of kernel@workload from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     measurement (profiles/traffic.json, copy-calibrated), or None."""
@@ -269,15 +311,38 @@ def main():
                                   dev.upload(inputs.uniform(9 + 100 * c, (desc.O,), -1, 1)), y) for c in range(3)]
                 tm = time_steps(dev, pc, sets_c, args.warmup, steps)
                 cfgs[key] = summarize(pc.describe().split(" kernels:")[0], pc, tm, "mfma", key=key)
+            # the reference's published convolution profiles (its only published numbers, M5 iPad
+            # GPU time): conv2d N1 256x256 C=O=512 3x3 at 9.71 TFLOP/s (AGENTS.md:23) and conv3d
+            # N1 D3 256x256 C=O=512 3x3x3 at 9.18 TFLOP/s (AGENTS.md:49-52; largeProfileDimensions,
+            # convolution3d.swift:1316-1334); no padding, stride 1; seeded U[-1,1) data
+            for key, dims, m5 in (("reference_profile_conv2d", dict(rank=2, N=1, D=1, H=256, W=256, C=512, O=512, KD=1,
+                                                                    KH=3, KW=3), 9.71),
+                                  ("reference_profile_conv3d", dict(rank=3, N=1, D=3, H=256, W=256, C=512, O=512, KD=3,
+                                                                    KH=3, KW=3), 9.18)):
+                desc = mtk.ConvDesc(stride_d=1, stride_h=1, stride_w=1, dil_d=1, dil_h=1, dil_w=1, has_bias=0,
+                                    dtype=mtk.F16, **dims)
+                pc = mtk.ConvPlan(dev, desc)
+                shape = pc.out_shape()
+                xs = (desc.N, desc.D, desc.H, desc.W, desc.C)
+                ws_ = (desc.KD, desc.KH, desc.KW, desc.C, desc.O)
+                y = dev.empty(int(np.prod(shape)) * 2)
+                sets_c = [pc.args(dev.upload(inputs.uniform(30 + 100 * c, xs, -1, 1)),
+                                  dev.upload(inputs.uniform(31 + 100 * c, ws_, -1, 1)), None, y) for c in range(3)]
+                tm = time_steps(dev, pc, sets_c, args.warmup, steps)
+                cfgs[key] = summarize(pc.describe().split(" kernels:")[0], pc, tm, "mfma", key=key)
+                cfgs[key]["reference_m5_tflops"] = m5
             # OIDHW -> DHWIO weight re-layout at the reference's profile shape (512 x 512, 3x3x3;
-            # AGENTS.md:51), HBM-bound: three rotating source copies
+            # AGENTS.md:51), HBM-bound: 40 rotating source copies (566 MB with the destination) so the
+            # 256 MB Infinity Cache cannot serve the repeats
             pp = mtk.PermutePlan(dev, 512, 512, 3, 3, 3)
             wsh = (512, 512, 3, 3, 3)
             dst = dev.empty(int(np.prod(wsh)) * 2)
-            sets_p = [pp.args(dev.upload(inputs.normal(14 + 100 * c, wsh)), dst) for c in range(3)]
+            wsrc = inputs.normal(14, wsh)
+            sets_p = [pp.args(dev.upload(wsrc), dst) for c in range(40)]
             tm = time_steps(dev, pp, sets_p, args.warmup, steps * 4)
             cfgs["conv_weight_permute"] = summarize("OIDHW -> DHWIO weight re-layout, O = C = 512, 3x3x3 (f16)", pp, tm,
                                                     "hbm", key="conv_weight_permute")
+            cfgs["conv_weight_permute"]["reference_m5_ms"] = 3.42  # AGENTS.md:51
             for causal in (False, True):
                 pa = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
                 shp = (2, 4096, 32, 128)
@@ -341,6 +406,9 @@ def main():
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         log(f"[bench] cpu baseline: {line['cpu_baseline']}")
+        if not args.quick:
+            line["cpu_baselines_other"] = cpu_baselines_other()
+            log(f"[bench] cpu baselines (other configs): {line['cpu_baselines_other']}")
     else:
         line["cpu_baseline"] = None
     dev.close()

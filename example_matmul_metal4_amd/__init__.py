@@ -35,7 +35,8 @@ import numpy as np
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(PKG, "lib")
-LIB_PATH = os.path.join(LIB_DIR, "libmtk.so")
+# $MTK_LIBRARY: another build of the same library (e.g. the host-sanitizer build the tests make)
+LIB_PATH = os.environ.get("MTK_LIBRARY") or os.path.join(LIB_DIR, "libmtk.so")
 
 MTK_OK = 0
 MTK_ERR_INVALID = -1

@@ -6,7 +6,8 @@ Outputs (under example_matmul_metal4_amd/lib/, git-ignored, shipped with the tre
   mtk_<unit>.hsaco   one code object per csrc/<unit>.hip, `hipcc --genco --offload-arch=gfx950`
                      (replaces the reference's package.sh `xcrun metal` -> metallib step,
                      Sources/matmul/package.sh:1-3, and its run-time makeLibrary(source:) JIT)
-  libmtk.so          host runtime (csrc/runtime.cpp) exporting include/mtk.h, linked to libamdhip64
+  libmtk.so          host runtime (csrc/runtime.cpp, plus any host HIP units compiled by hipcc)
+                     exporting include/mtk.h, linked to libamdhip64
 """
 from __future__ import annotations
 
@@ -49,13 +50,28 @@ def hip_unit(unit: str) -> str:
     return out
 
 
+# Host sources compiled by hipcc into the library itself (host code plus a gfx950 device part).
+HOST_HIP_UNITS: list[str] = []
+
+
+def host_hip_object(unit: str) -> str:
+    out = os.path.join(LIB, f"{unit}.o")
+    tmp = out + ".tmp"
+    _run([os.path.join(ROCM, "bin", "hipcc"), "-c", "-fPIC", "--offload-arch=gfx950", "-O2", "-std=c++17",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          os.path.join(CSRC, unit + ".hip"), "-o", tmp])
+    os.replace(tmp, out)
+    return out
+
+
 def host_lib() -> str:
     out = os.path.join(LIB, "libmtk.so")
     tmp = out + ".tmp"
+    objs = [host_hip_object(u) for u in HOST_HIP_UNITS]
     cxx = shutil.which("g++") or "g++"
     _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
-          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", os.path.join(CSRC, "runtime.cpp"),
-          f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl", "-o", tmp])
+          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", os.path.join(CSRC, "runtime.cpp")] + objs +
+         [f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl", "-o", tmp])
     os.replace(tmp, out)
     return out
 

@@ -1130,6 +1130,19 @@ int mtk_graph_create(const mtk_plan *p, const void *arg_sets, int nsets, int ste
     (void)hipGraphDestroy(graph);
     return fail(MTK_ERR_HIP, "graph instantiation failed: %s", hipGetErrorString(ei));
   }
+  // Finish setting the graph up on the device now (kernel argument blocks and the launch packets
+  // prepared), so that the first launch submits work instead of doing this set-up. No kernel runs.
+  const hipError_t eu = hipGraphUpload(exec, st);
+  if (eu == hipSuccess) {
+    const hipError_t es = hipStreamSynchronize(st);
+    if (es != hipSuccess) {
+      (void)hipGraphExecDestroy(exec);
+      (void)hipGraphDestroy(graph);
+      return fail(MTK_ERR_HIP, "graph upload failed: %s", hipGetErrorString(es));
+    }
+  } else {
+    (void)hipGetLastError();  // optional step: the first launch then does the set-up itself
+  }
   mtk_graph *g = new mtk_graph();
   g->ctx = p->ctx;
   g->stream = st;
@@ -1172,26 +1185,40 @@ int mtk_profile(const mtk_plan *p, const void *arg_sets, int nsets, int warmup, 
     if (s != MTK_OK) return s;
   }
   const size_t nk = p->launches.size();
-  std::vector<hipEvent_t> evs((size_t)iters * (nk + 1));
-  for (auto &e : evs) HIP_TRY(hipEventCreate(&e));
+  // Events created so far are destroyed on every exit path; a failed query fails the call (never
+  // a silent 0 ms).
+  std::vector<hipEvent_t> evs;
+  evs.reserve((size_t)iters * (nk + 1));
   int status = MTK_OK;
+  for (size_t i = 0; i < (size_t)iters * (nk + 1) && status == MTK_OK; ++i) {
+    hipEvent_t e = nullptr;
+    const hipError_t ec = hipEventCreate(&e);
+    if (ec != hipSuccess)
+      status = fail(MTK_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(ec));
+    else
+      evs.push_back(e);
+  }
   for (int i = 0; i < iters && status == MTK_OK; ++i)
     status = launch_all(p, bound[(size_t)(i % nsets)], &evs[(size_t)i * (nk + 1)]);
   if (status == MTK_OK) {
     hipError_t e = hipStreamSynchronize(p->ctx->stream);
     if (e != hipSuccess) status = fail(MTK_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
   }
+  auto elapsed = [&](hipEvent_t a, hipEvent_t b, float *ms) {
+    const hipError_t e = hipEventElapsedTime(ms, a, b);
+    return e == hipSuccess ? MTK_OK : fail(MTK_ERR_HIP, "hipEventElapsedTime: %s", hipGetErrorString(e));
+  };
   if (status == MTK_OK) {
     std::vector<double> per(nk, 0.0);
-    for (int i = 0; i < iters; ++i) {
-      for (size_t k = 0; k < nk; ++k) {
+    for (int i = 0; i < iters && status == MTK_OK; ++i) {
+      for (size_t k = 0; k < nk && status == MTK_OK; ++k) {
         float ms = 0;
-        (void)hipEventElapsedTime(&ms, evs[(size_t)i * (nk + 1) + k], evs[(size_t)i * (nk + 1) + k + 1]);
+        status = elapsed(evs[(size_t)i * (nk + 1) + k], evs[(size_t)i * (nk + 1) + k + 1], &ms);
         per[k] += ms;
       }
     }
     float total = 0;
-    (void)hipEventElapsedTime(&total, evs[0], evs[(size_t)(iters - 1) * (nk + 1) + nk]);
+    if (status == MTK_OK) status = elapsed(evs[0], evs[(size_t)(iters - 1) * (nk + 1) + nk], &total);
     out->total_ms = total / iters;
     out->n_kernels = (int)std::min<size_t>(nk, 4);
     for (size_t k = 0; k < nk && k < 4; ++k) {

@@ -146,7 +146,7 @@ int mtk_gemm_plan(mtk_ctx *ctx, const mtk_gemm_desc *desc, mtk_plan **out);
 typedef struct {
   const void *A, *B, *bias;
   void *C;
-  void *workspace; /* >= mtk_plan_workspace_bytes(plan) bytes, 256-byte aligned, or NULL if 0 */
+  void *workspace; /* >= mtk_plan_workspace_bytes(plan) bytes, 16-byte aligned, or NULL if 0 */
 } mtk_gemm_args;
 
 /* Replaces setBuffer(0..3) + dispatchThreadgroups (+ the reduce_sum_2 encoder)

@@ -24,12 +24,17 @@ def _f64(x, dtype):
     return oracle.to_f32(x, dtype).astype(np.float64)
 
 
+def _bhsd(x, dtype):
+    """[B][S][H][D] -> float64 [B][H][S][D] (batched BLAS products below)."""
+    return np.ascontiguousarray(_f64(x, dtype).transpose(0, 2, 1, 3))
+
+
 def _magnitudes(Q, K, V, G, causal, dtype):
     """float64 P, |dS| and the per-row D magnitude for the tolerance bound, [B][H][Sq][Skv]."""
-    q, k, v, g = (_f64(x, dtype) for x in (Q, K, V, G))
-    B, Sq, H, D = q.shape
-    Skv = k.shape[1]
-    s = np.einsum("bihd,bjhd->bhij", q, k) / np.sqrt(D)
+    q, k, v, g = (_bhsd(x, dtype) for x in (Q, K, V, G))
+    B, H, Sq, D = q.shape
+    Skv = k.shape[2]
+    s = (q @ k.transpose(0, 1, 3, 2)) / np.sqrt(D)
     vis = np.ones((Sq, Skv), bool)
     if causal:
         vis = np.arange(Skv)[None, :] <= (np.arange(Sq)[:, None] + (Skv - Sq))
@@ -37,15 +42,14 @@ def _magnitudes(Q, K, V, G, causal, dtype):
     m = np.max(s, -1, keepdims=True)
     m = np.where(np.isfinite(m), m, 0.0)
     p = np.where(vis[None, None], np.exp(s - m), 0.0)
+    del s
     den = p.sum(-1, keepdims=True)
     p = np.where(den > 0, p / np.where(den > 0, den, 1), 0.0)
-    o = np.einsum("bhij,bjhd->bhid", p, v)
-    go = g.transpose(0, 2, 1, 3)
-    dd = np.sum(o * go, -1, keepdims=True)
-    dp = np.einsum("bhid,bjhd->bhij", go, v)
-    ds = p * (dp - dd) / np.sqrt(D)
-    dmag = np.sum(np.abs(o * go), -1, keepdims=True)  # [B][H][Sq][1]
-    return p, np.abs(ds), dmag
+    o = p @ v
+    dd = np.sum(o * g, -1, keepdims=True)
+    ds = np.abs(p * ((g @ v.transpose(0, 1, 3, 2)) - dd) / np.sqrt(D))
+    dmag = np.sum(np.abs(o * g), -1, keepdims=True)  # [B][H][Sq][1]
+    return p, ds, dmag
 
 
 def _check(name, got, exp, bound_terms, dtype):
@@ -91,12 +95,14 @@ def _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=90, pairs=None, Hkv=N
         dQ, dK, dV, eQ, eK, eV = (sub(x) for x in (dQ, dK, dV, eQ, eK, eV))
     p, ads, dmag = _magnitudes(Q, K, V, G, causal, dtype)
     s = 1.0 / np.sqrt(D)
-    q, k, g = (np.abs(_f64(x, dtype)) for x in (Q, K, G))
+    q, k, g = (np.abs(_bhsd(x, dtype)) for x in (Q, K, G))
     w = ads + s * p * dmag  # [B][H][Sq][Skv]
+    del ads
+    back = lambda t: t.transpose(0, 2, 1, 3)  # [B][H][S][D] -> [B][S][H][D]
     per_group = lambda t: t.reshape(t.shape[0], t.shape[1], -1, group, D).sum(3)  # sum a group's query heads
-    _check("dV", dV[sel], eV, per_group(np.einsum("bhij,bihd->bjhd", p, g)), dtype)
-    _check("dK", dK[sel], eK, per_group(np.einsum("bhij,bihd->bjhd", w, q)), dtype)
-    _check("dQ", dQ[sel], eQ, np.einsum("bhij,bjhd->bihd", w, k), dtype)
+    _check("dV", dV[sel], eV, per_group(back(p.transpose(0, 1, 3, 2) @ g)), dtype)
+    _check("dK", dK[sel], eK, per_group(back(w.transpose(0, 1, 3, 2) @ q)), dtype)
+    _check("dQ", dQ[sel], eQ, back(w @ k), dtype)
 
 
 @pytest.mark.parametrize("B,H,Sq,Skv,causal,dtype", [
@@ -125,9 +131,10 @@ def test_attention_bwd_grouped_kv_heads(dev, B, H, Hkv, Sq, Skv, causal, dtype):
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_attention_bwd_config5_full_size(dev, causal):
-    # BASELINE config 5 shape (B=2, H=32, S=4096, D=128); every output must be finite, and two
-    # (b, h) pairs are checked element by element against the oracle (which costs ~S^2 D per pair).
-    _run_and_check(dev, 2, 32, 4096, 4096, causal, "f16", seed=10, pairs=(37, 39))
+    # BASELINE config 5 shape (B=2, H=32, S=4096, D=128); every output must be finite, and eight
+    # (b, h) pairs (both batches: b=0 h=28..31, b=1 h=0..3) are checked element by element against
+    # the oracle (which costs ~S^2 D per pair).
+    _run_and_check(dev, 2, 32, 4096, 4096, causal, "f16", seed=10, pairs=(28, 36))
 
 
 @pytest.mark.parametrize("q_rows", [128, 256])

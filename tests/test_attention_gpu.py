@@ -124,25 +124,35 @@ def test_grouped_kv_heads(dev, H, Hkv, causal, q_rows):
     assert np.array_equal(got.view(np.uint16), full.view(np.uint16))
 
 
-def test_config5_full_size_sampled_rows(dev):
+def _probs_rows_f64(Q, K, r0, r1, causal):
+    """float64 softmax probabilities of query rows r0..r1-1, [B][H][rows][S_kv] (BLAS products)."""
+    q = Q[:, r0:r1].astype(np.float64).transpose(0, 2, 1, 3)  # [B][H][rows][D]
+    k = K.astype(np.float64).transpose(0, 2, 3, 1)            # [B][H][D][S_kv]
+    s = (q @ k) / np.sqrt(Q.shape[3])
+    if causal:  # rows r0.. see keys j <= i (S_q == S_kv)
+        s = np.where(np.arange(K.shape[1])[None, :] > np.arange(r0, r1)[:, None], -np.inf, s)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    return p / p.sum(-1, keepdims=True)
+
+
+def test_config5_full_size(dev):
     # BASELINE config 5: B=2, H=32, S=4096, D=128, Q,K,V ~ N(0,1), scale 1/sqrt(D); both masks.
+    # 512 query rows of every (b, h) per mask (8 blocks of 64 spread over the sequence, first and
+    # last included) against the oracle, element by element.
     B, S, H = 2, 4096, 32
     Q, K, V = qkv(10, B, S, H)
-    rows = (np.r_[0:32], np.r_[2032:2064], np.r_[4064:4096])
+    absv = np.abs(V.astype(np.float64)).transpose(0, 2, 1, 3)  # [B][H][S][D]
+    starts = np.linspace(0, S - 64, 8).astype(int)
     for causal in (False, True):
         got = mtk.attention(dev, Q, K, V, causal=causal)
-        for r in rows:
-            r0, r1 = int(r[0]), int(r[-1]) + 1
+        worst = 0.0
+        for r0 in starts:
+            r0 = int(r0)
+            r1 = r0 + 64
             exp = oracle.attention(Q, K, V, causal=causal, rows=(r0, r1))[:, r0:r1]
-            p = probs_f64(Q[:, r0:r1], K, False) if not causal else None
-            if causal:  # rows r0.. see keys j <= i
-                q = Q[:, r0:r1].astype(np.float64)
-                k = K.astype(np.float64)
-                s = np.einsum("bihd,bjhd->bhij", q, k) / np.sqrt(128)
-                s = np.where(np.arange(S)[None, :] > np.arange(r0, r1)[:, None], -np.inf, s)
-                p = np.exp(s - s.max(-1, keepdims=True))
-                p /= p.sum(-1, keepdims=True)
-            abspv = np.einsum("bhij,bjhd->bihd", p, np.abs(V.astype(np.float64)))
+            abspv = (_probs_rows_f64(Q, K, r0, r1, causal) @ absv).transpose(0, 2, 1, 3)
             res = oracle.compare(got[:, r0:r1].astype(np.float64), exp, bound=oracle.ulp(exp) + 2.0 ** -10 * abspv)
-            print(f"[attn] config5 causal={causal} rows {r0}:{r1} {res}", flush=True)
-            assert res["ok"], res
+            assert res["ok"], (causal, r0, res)
+            worst = max(worst, res["worst_ratio"])
+        print(f"[attn] config5 causal={causal}: 512 rows per (b, h) within bound, worst err/bound {worst:.3f}",
+              flush=True)
