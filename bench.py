@@ -394,6 +394,21 @@ def main():
             cfgs["config5_attn_bwd_gqa8"] = summarize(
                 "config 5 shape with 8 K/V heads (H=32, H_kv=8), flash-attn backward", pgb, tm, "mfma",
                 key="config5_bwd_gqa8")
+            # other head dimensions at the config 5 shape (the reference's run(headDimension:),
+            # attention.swift:398): D = 64 and D = 256, both masks
+            for hd in (64, 256):
+                shp_d = (2, 4096, 32, hd)
+                o = dev.empty(int(np.prod(shp_d)) * 2)
+                sets_d = [None, None]
+                for c in range(2):
+                    sets_d[c] = (dev.upload(inputs.normal(10 + 100 * c, shp_d)), dev.upload(inputs.normal(11 + 100 * c, shp_d)),
+                                 dev.upload(inputs.normal(12 + 100 * c, shp_d)))
+                for causal in (False, True):
+                    pd = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, hd, causal=causal)
+                    tm = time_steps(dev, pd, [pd.args(*t_, o) for t_ in sets_d], args.warmup, steps)
+                    key = f"config5_attn_d{hd}" + ("_causal" if causal else "")
+                    cfgs[key] = summarize(f"config 5 shape, head dimension {hd}, flash-attn fwd "
+                                          f"{'causal' if causal else 'non-causal'}", pd, tm, "mfma", key=key)
         except Exception as e:  # report what was measured; the headline stands on its own
             cfgs["error"] = repr(e)
         line["configs"] = cfgs

@@ -403,7 +403,7 @@ class GemmPlan(_Plan):
 
 class AttentionPlan(_Plan):
     """O = softmax(Q K^T / sqrt(D)) V per (batch, head); Q, O [B][S_q][H][D], K, V [B][S_kv][H_kv][D]
-    (H_kv = 0: H; query head h reads K/V head h // (H // H_kv)), D = 128."""
+    (H_kv = 0: H; query head h reads K/V head h // (H // H_kv)), head dimension D = 1..256."""
 
     _args_type = AttnArgs
     _run_fn = "mtk_attn_run"

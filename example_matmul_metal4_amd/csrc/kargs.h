@@ -9,7 +9,7 @@
 
 #include <stdint.h>
 
-#define MTK_KARGS_VERSION 7
+#define MTK_KARGS_VERSION 8
 
 /* Tile-GEMM kernels: plain GEMM (A [M][K] . B, B either [N][K] or [K][N]) and
  * implicit-GEMM convolution (A = im2col of an NDHWC activation, B = DHWIO
@@ -76,7 +76,8 @@ typedef struct {
   int32_t has_bias;
 } mtk_skinny_args;
 
-/* Flash-attention forward, Q/K/V/O laid out [B][S][H][D] with D = 128. */
+/* Flash-attention forward, Q/K/V/O laid out [B][S][H][D]; the kernel is compiled for a padded head
+   dimension (64, 128 or 256) and runs any D up to it. */
 typedef struct {
   const void *Q;
   const void *K;
@@ -89,6 +90,7 @@ typedef struct {
   uint32_t q_bytes, kv_bytes;
   float *lse; /* [B][H][S_q] natural-log row log-sum-exp of the scaled scores, or NULL */
   int32_t H_kv; /* K/V heads (divides H): query head h reads K/V head h / (H / H_kv) */
+  int32_t D;    /* head dimension */
 } mtk_attn_kargs;
 
 /* Flash-attention backward (all three kernels of the plan take this block). */

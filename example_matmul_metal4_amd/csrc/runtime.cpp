@@ -47,7 +47,8 @@ int fail(int status, const char *fmt, ...) {
   } while (0)
 
 constexpr uint64_t kMaxOperandBytes = (1ull << 31) - 256;  // buffer-resource ranges (see device.hpp)
-constexpr int kAutoKStagger = 16;  // in-workgroup split-K: boundary offsets span up to 16 K-tiles
+constexpr int kAutoKStagger = 16;
+constexpr int kMaxHeadDim = MTK_ATTN_MAX_HEAD_DIM;  // largest padded head dimension compiled (256)  // in-workgroup split-K: boundary offsets span up to 16 K-tiles
 
 }  // namespace
 
@@ -639,10 +640,13 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   if (d.H_kv == 0) d.H_kv = d.H;
   if (d.H_kv < 0 || d.H % d.H_kv != 0)
     return fail(MTK_ERR_INVALID, "H_kv must divide H (got H=%d, H_kv=%d)", d.H, d.H_kv);
-  if (d.D != 128) return fail(MTK_ERR_UNSUPPORTED, "head dimension must be 128 (got %d)", d.D);
+  if (d.D < 1 || d.D > kMaxHeadDim)
+    return fail(MTK_ERR_UNSUPPORTED, "head dimension must be 1..%d (got %d)", kMaxHeadDim, d.D);
   if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "attention dtype must be MTK_F16 or MTK_BF16");
   if (d.q_rows != 0 && d.q_rows != 128 && d.q_rows != 256)
     return fail(MTK_ERR_INVALID, "q_rows must be 0, 128 or 256 (got %d)", d.q_rows);
+  if (d.q_rows == 256 && d.D != 128)
+    return fail(MTK_ERR_UNSUPPORTED, "q_rows 256 (the ping-pong kernel) needs head dimension 128 (got %d)", d.D);
   const uint64_t q_bytes = (uint64_t)d.B * d.S_q * d.H * d.D * 2;
   const uint64_t kv_bytes = (uint64_t)d.B * d.S_kv * d.H_kv * d.D * 2;
   if (q_bytes > kMaxOperandBytes || kv_bytes > kMaxOperandBytes)
@@ -651,7 +655,12 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   p->ctx = ctx;
   p->kind = PLAN_ATTN;
   p->attn = d;
-  p->align_a = p->align_b = 16;
+  // Head dimension: the kernels are compiled for a padded head dimension DP of 64, 128 or 256 and
+  // run any D <= DP. D % 8 == 0 keeps every row 16-byte aligned (direct-to-LDS staging, 16-byte
+  // loads); other D use the element-staged kernels (2-byte aligned rows).
+  const int dp = d.D <= 64 ? 64 : d.D <= 128 ? 128 : 256;
+  const bool gen = d.D % 8 != 0;
+  p->align_a = p->align_b = gen ? 2 : 16;
   // Query rows per workgroup: 256 (the ping-pong kernel: 8 wavefronts in two groups alternating MFMA
   // and softmax blocks, one workgroup per CU) when its grid still fills the device and the mask is
   // not causal; 128 (4 wavefronts, two workgroups per CU) otherwise: with causal masking the larger
@@ -659,11 +668,15 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   int rows = d.q_rows;
   if (rows == 0) {
     const int cus = ctx ? ctx->prop.multiProcessorCount : 256;
-    rows = (!d.causal && (long long)d.B * d.H * ((d.S_q + 255) / 256) >= cus) ? 256 : 128;
+    rows = (d.D == 128 && !d.causal && (long long)d.B * d.H * ((d.S_q + 255) / 256) >= cus) ? 256 : 128;
   }
   Launch g;
-  g.name = std::string("mtk_attn_fwd_") + (rows == 256 ? "pp_" : "") + (d.dtype == MTK_F16 ? "f16" : "bf16") +
-           (d.causal ? "_causal" : "");
+  std::string family = rows == 256 ? "pp_" : "";
+  if (gen)
+    family = "g" + std::to_string(dp) + "_";
+  else if (dp != 128)
+    family = "d" + std::to_string(dp) + "_";
+  g.name = "mtk_attn_fwd_" + family + (d.dtype == MTK_F16 ? "f16" : "bf16") + (d.causal ? "_causal" : "");
   if (rows == 256) g.block = 512;  // 8 wavefronts: two groups of 4 in ping-pong
   mtk_attn_kargs a{};
   a.B = d.B;
@@ -676,6 +689,7 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)d.D));
   a.q_bytes = (uint32_t)q_bytes;
   a.kv_bytes = (uint32_t)kv_bytes;
+  a.D = d.D;
   g.grid = (unsigned)((long long)a.q_blocks * d.B * d.H);
   set_args(g, a);
   p->launches.push_back(g);
@@ -788,8 +802,9 @@ int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
   } else {
     const mtk_attn_args *t = (const mtk_attn_args *)argset;
     if (!t || !t->Q || !t->K || !t->V || !t->O) return fail(MTK_ERR_INVALID, "Q, K, V and O must be non-null");
-    if (!aligned(t->Q, 16) || !aligned(t->K, 16) || !aligned(t->V, 16) || !aligned(t->O, 16))
-      return fail(MTK_ERR_INVALID, "Q, K, V, O must be 16-byte aligned");
+    const unsigned al = p->align_a;
+    if (!aligned(t->Q, al) || !aligned(t->K, al) || !aligned(t->V, al) || !aligned(t->O, al))
+      return fail(MTK_ERR_INVALID, "Q, K, V, O must be %u-byte aligned for this plan", al);
     if (t->lse && !aligned(t->lse, 4)) return fail(MTK_ERR_INVALID, "lse must be 4-byte aligned");
     mtk_attn_kargs &a = args_of<mtk_attn_kargs>(ls[0]);
     a.Q = t->Q;

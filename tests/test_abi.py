@@ -268,8 +268,20 @@ def test_attention_select_and_validation():
     flops = p.work()[0]
     assert flops == 4 * 2 * 32 * 128 * (4096 * 4097 // 2)
     assert mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128).work()[0] == 549755813888
-    with pytest.raises(mtk.MtkError) as e:
-        mtk.AttentionPlan(None, 1, 1, 16, 16, 64)
+    # head dimensions (the reference's K, any value: attention.swift:398): padded kernel families
+    for D, fam in ((64, "d64_"), (8, "d64_"), (96, ""), (136, "d256_"), (256, "d256_"), (1, "g64_"), (100, "g128_"),
+                   (255, "g256_")):
+        p = mtk.AttentionPlan(None, 1, 2, 300, 300, D)
+        assert p.describe().endswith(f"kernels: mtk_attn_fwd_{fam}f16"), (D, p.describe())
+        assert p.work()[0] == 4 * 2 * D * 300 * 300
+    assert mtk.AttentionPlan(None, 2, 32, 4096, 4096, 64, causal=True).describe().endswith("mtk_attn_fwd_d64_f16_causal")
+    for D, q_rows, status in ((257, 0, mtk.MTK_ERR_UNSUPPORTED), (0, 0, mtk.MTK_ERR_UNSUPPORTED),
+                              (64, 256, mtk.MTK_ERR_UNSUPPORTED)):
+        with pytest.raises(mtk.MtkError) as e:
+            mtk.AttentionPlan(None, 1, 1, 16, 16, D, q_rows=q_rows)
+        assert e.value.status == status
+    with pytest.raises(mtk.MtkError) as e:  # the backward: D = 128 only
+        mtk.AttentionBwdPlan(None, 1, 1, 16, 16, 64)
     assert e.value.status == mtk.MTK_ERR_UNSUPPORTED
     with pytest.raises(mtk.MtkError) as e:
         mtk.AttentionPlan(None, 0, 1, 16, 16, 128)

@@ -155,11 +155,13 @@ def attention_f64(Q, K, V, causal):
     return np.einsum("bhij,bjhd->bihd", p, v), p
 
 
+# head dimensions: the reference's run(headDimension:) takes any value (attention.swift:398)
+@pytest.mark.parametrize("D", [1, 3, 24, 64, 96, 200, 256])
 @pytest.mark.parametrize("causal", [False, True])
-def test_attention_random_vs_float64(orc, causal):
-    Q = orc.normal(20, (2, 45, 3, 64))
-    K = orc.normal(21, (2, 45, 3, 64))
-    V = orc.normal(22, (2, 45, 3, 64))
+def test_attention_random_vs_float64(orc, causal, D):
+    Q = orc.normal(20, (2, 45, 3, D))
+    K = orc.normal(21, (2, 45, 3, D))
+    V = orc.normal(22, (2, 45, 3, D))
     ref, p = attention_f64(Q, K, V, causal)
     got = orc.attention(Q, K, V, causal=causal)
     absv = np.einsum("bhij,bjhd->bihd", p, np.abs(V.astype(np.float64)))
