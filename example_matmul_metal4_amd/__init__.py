@@ -148,6 +148,7 @@ SIGNATURES = {
     "mtk_set_stream": (ctypes.c_int, [_VP, _VP]),
     "mtk_gemm_plan": (ctypes.c_int, [_VP, ctypes.POINTER(GemmDesc), _PP]),
     "mtk_gemm_run": (ctypes.c_int, [_VP, ctypes.POINTER(GemmArgs)]),
+    "mtk_gemm_run_noalloc": (ctypes.c_int, [_VP, ctypes.POINTER(GemmArgs)]),
     "mtk_attn_plan": (ctypes.c_int, [_VP, ctypes.POINTER(AttnDesc), _PP]),
     "mtk_attn_run": (ctypes.c_int, [_VP, ctypes.POINTER(AttnArgs)]),
     "mtk_attn_bwd_plan": (ctypes.c_int, [_VP, ctypes.POINTER(AttnDesc), _PP]),

@@ -51,7 +51,7 @@ def hip_unit(unit: str) -> str:
 
 
 # Host sources compiled by hipcc into the library itself (host code plus a gfx950 device part).
-HOST_HIP_UNITS: list[str] = []
+HOST_HIP_UNITS: list[str] = ["scratch"]  # the static device scratch of mtk_gemm_run_noalloc
 
 
 def host_hip_object(unit: str) -> str:

@@ -25,6 +25,7 @@
 
 #include "../../include/mtk.h"
 #include "kargs.h"
+#include "scratch.h"
 
 namespace {
 
@@ -718,42 +719,52 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
 
 // ------------------------------------------------------------------ binding run-time pointers
 
+int check_gemm_args(const mtk_plan *p, const mtk_gemm_args *g) {
+  if (!g || !g->A || !g->B || !g->C) return fail(MTK_ERR_INVALID, "A, B and C must be non-null");
+  if (p->gemm.has_bias && !g->bias) return fail(MTK_ERR_INVALID, "plan has a bias but bias is null");
+  if (!aligned(g->A, p->align_a) || !aligned(g->B, p->align_b))
+    return fail(MTK_ERR_INVALID, "A/B must be %u-byte aligned for this plan", p->align_a);
+  if (!aligned(g->C, 4)) return fail(MTK_ERR_INVALID, "C must be 4-byte aligned");
+  return MTK_OK;
+}
+
+// Writes the run-time pointers of one GEMM launch into `block`, a copy of that launch's argument
+// block; `ws` is the workspace (the caller's, or the static scratch).
+void patch_gemm(const mtk_plan *p, const Launch &l, char *block, const mtk_gemm_args *g, void *ws) {
+  if (l.name.rfind("mtk_skinny_", 0) == 0) {
+    mtk_skinny_args *k = (mtk_skinny_args *)block;
+    k->A = g->A;
+    k->B = g->B;
+    k->bias = g->bias;
+    k->C = g->C;
+    return;
+  }
+  const bool two_pass = p->workspace != 0 && !p->serial_split;
+  if (l.role == ROLE_MAIN) {
+    mtk_tile_args *a = (mtk_tile_args *)block;
+    a->A = g->A;
+    a->B = g->B;
+    a->bias = g->bias;
+    a->C = two_pass ? nullptr : g->C;
+    a->partial = p->workspace ? (float *)ws : nullptr;
+  } else if (l.role == ROLE_REDUCE) {
+    mtk_reduce_args *r = (mtk_reduce_args *)block;
+    r->partial = (const float *)ws;
+    r->bias = g->bias;
+    r->C = g->C;
+    r->vec4 = r->vec4 && aligned(g->C, 8) && (!g->bias || aligned(g->bias, 8));
+  }
+}
+
 int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
   ls = p->launches;
   if (p->kind == PLAN_GEMM) {
     const mtk_gemm_args *g = (const mtk_gemm_args *)argset;
-    if (!g || !g->A || !g->B || !g->C) return fail(MTK_ERR_INVALID, "A, B and C must be non-null");
-    if (p->gemm.has_bias && !g->bias) return fail(MTK_ERR_INVALID, "plan has a bias but bias is null");
-    if (!aligned(g->A, p->align_a) || !aligned(g->B, p->align_b))
-      return fail(MTK_ERR_INVALID, "A/B must be %u-byte aligned for this plan", p->align_a);
-    if (!aligned(g->C, 4)) return fail(MTK_ERR_INVALID, "C must be 4-byte aligned");
+    int s = check_gemm_args(p, g);
+    if (s != MTK_OK) return s;
     if (p->workspace && (!g->workspace || !aligned(g->workspace, 16)))
       return fail(MTK_ERR_INVALID, "this plan needs a 16-byte aligned workspace of %zu bytes", p->workspace);
-    if (ls[0].name.rfind("mtk_skinny_", 0) == 0) {
-      mtk_skinny_args &k = args_of<mtk_skinny_args>(ls[0]);
-      k.A = g->A;
-      k.B = g->B;
-      k.bias = g->bias;
-      k.C = g->C;
-      return MTK_OK;
-    }
-    const bool two_pass = p->workspace != 0 && !p->serial_split;
-    for (Launch &l : ls) {
-      if (l.role == ROLE_MAIN) {
-        mtk_tile_args &a = args_of<mtk_tile_args>(l);
-        a.A = g->A;
-        a.B = g->B;
-        a.bias = g->bias;
-        a.C = two_pass ? nullptr : g->C;
-        a.partial = p->workspace ? (float *)g->workspace : nullptr;
-      } else if (l.role == ROLE_REDUCE) {
-        mtk_reduce_args &r = args_of<mtk_reduce_args>(l);
-        r.partial = (const float *)g->workspace;
-        r.bias = g->bias;
-        r.C = g->C;
-        r.vec4 = r.vec4 && aligned(g->C, 8) && (!g->bias || aligned(g->bias, 8));
-      }
-    }
+    for (Launch &l : ls) patch_gemm(p, l, l.args.data(), g, g->workspace);
   } else if (p->kind == PLAN_CONV) {
     const mtk_conv_args *c = (const mtk_conv_args *)argset;
     if (!c || !c->x || !c->w || !c->y) return fail(MTK_ERR_INVALID, "x, w and y must be non-null");
@@ -913,6 +924,9 @@ int mtk_init(int device, const char *code_object_dir, mtk_ctx **out) {
   if (hipGetDeviceProperties(&ctx->prop, device) != hipSuccess) return bail(fail(MTK_ERR_HIP, "hipGetDeviceProperties failed"));
   if (strncmp(ctx->prop.gcnArchName, "gfx950", 6) != 0)
     return bail(fail(MTK_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950 (MI355X)", device, ctx->prop.gcnArchName));
+  // the static scratch of mtk_gemm_run_noalloc: its device address on this device, taken once
+  // (a failure is reported by that entry point; nothing else uses the scratch)
+  (void)mtk_scratch::setup(device);
   if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess)
     return bail(fail(MTK_ERR_HIP, "hipStreamCreate failed"));
   ctx->stream = ctx->own_stream;
@@ -1050,6 +1064,38 @@ int mtk_gemm_plan(mtk_ctx *ctx, const mtk_gemm_desc *desc, mtk_plan **out) { ret
 int mtk_gemm_run(const mtk_plan *plan, const mtk_gemm_args *args) {
   if (plan && plan->kind != PLAN_GEMM) return fail(MTK_ERR_INVALID, "not a GEMM plan");
   return run_plan(plan, args);
+}
+
+int mtk_gemm_run_noalloc(const mtk_plan *plan, const mtk_gemm_args *args) {
+  if (!plan) return fail(MTK_ERR_INVALID, "null plan");
+  if (plan->kind != PLAN_GEMM) return fail(MTK_ERR_INVALID, "not a GEMM plan");
+  if (!plan->ctx) return fail(MTK_ERR_INVALID, "plan was created without a context (dry plan)");
+  int s = check_gemm_args(plan, args);
+  if (s != MTK_OK) return s;
+  if (args->workspace)
+    return fail(MTK_ERR_INVALID, "mtk_gemm_run_noalloc works in the library's static scratch: workspace must be NULL");
+  if (plan->workspace > (size_t)MTK_NOALLOC_MAX_WORKSPACE)
+    return fail(MTK_ERR_UNSUPPORTED,
+                "this plan needs a %zu-byte workspace, above the %zu bytes of mtk_gemm_run_noalloc's static scratch: "
+                "use mtk_gemm_run with a caller workspace",
+                plan->workspace, (size_t)MTK_NOALLOC_MAX_WORKSPACE);
+  void *ws = nullptr;
+  if (plan->workspace) {
+    char err[256];
+    if (mtk_scratch::address(plan->ctx->device, &ws, err, sizeof err) != 0) return fail(MTK_ERR_HIP, "%s", err);
+  }
+  // argument blocks on the stack: nothing is allocated, on the device or the host
+  alignas(16) char block[512];
+  HIP_TRY(hipSetDevice(plan->ctx->device));
+  for (const Launch &l : plan->launches) {
+    if (l.args.size() > sizeof block) return fail(MTK_ERR_INVALID, "argument block of %s too large", l.name.c_str());
+    memcpy(block, l.args.data(), l.args.size());
+    patch_gemm(plan, l, block, args, ws);
+    void *params[] = {block};
+    hipError_t e = hipModuleLaunchKernel(l.fn, l.grid, 1, 1, l.block, 1, 1, 0, plan->ctx->stream, params, nullptr);
+    if (e != hipSuccess) return fail(MTK_ERR_LAUNCH, "launch of %s failed: %s", l.name.c_str(), hipGetErrorString(e));
+  }
+  return MTK_OK;
 }
 
 int mtk_attn_plan(mtk_ctx *ctx, const mtk_attn_desc *desc, mtk_plan **out) { return plan_attn(ctx, desc, out); }

@@ -153,6 +153,19 @@ typedef struct {
  * (matmul.swift:427-474). Enqueues; does not wait. */
 int mtk_gemm_run(const mtk_plan *plan, const mtk_gemm_args *args);
 
+/* mtk_gemm_run without a caller workspace and without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The plan's workspace (split-K partials or
+ * running sums) is a static device array of MTK_NOALLOC_MAX_WORKSPACE bytes inside the library,
+ * one per GPU the library is initialised on, held until the process ends; args->workspace must be
+ * NULL. Plans whose mtk_plan_workspace_bytes exceeds the maximum return MTK_ERR_UNSUPPORTED (use
+ * mtk_gemm_run with a caller workspace). Same kernels and same results, bit for bit, as
+ * mtk_gemm_run. Every call on one GPU shares that GPU's array and no kernel needs it cleared
+ * (each writes before it reads): calls that overlap on one GPU (several streams or host threads
+ * at once) race on it and must be serialised by the caller. */
+#define MTK_NOALLOC_MAX_WORKSPACE (64u << 20)
+int mtk_gemm_run_noalloc(const mtk_plan *plan, const mtk_gemm_args *args);
+
 /* ------------------------------------------------------------------ attention */
 
 /* Replaces BlockDimenions / AttentionDimensions{R, C, K, Hq, Hk} and the R,C,Hq,Hk function
