@@ -331,6 +331,21 @@ def main():
                 tm = time_steps(dev, pc, sets_c, args.warmup, steps)
                 cfgs[key] = summarize(pc.describe().split(" kernels:")[0], pc, tm, "mfma", key=key)
                 cfgs[key]["reference_m5_tflops"] = m5
+                if desc.rank == 3:
+                    # the reference's permute + conv3d session at this shape (AGENTS.md:49-53: 9.07
+                    # TFLOP/s on M5): OIDHW weights re-laid out in the workspace by each run, then the
+                    # same convolution; TFLOP/s counts the convolution's FLOPs only, as there
+                    desc.weight_layout = mtk.WEIGHTS_OIDHW
+                    pf = mtk.ConvPlan(dev, desc)
+                    ws_f = dev.empty(pf.workspace_bytes)
+                    sets_f = [pf.args(sc.x, dev.upload(inputs.uniform(31 + 100 * c, (desc.O, desc.C, desc.KD, desc.KH,
+                                                                                       desc.KW), -1, 1)),
+                                      None, y, ws_f) for c, sc in enumerate(sets_c)]
+                    tm = time_steps(dev, pf, sets_f, args.warmup, steps)
+                    s = summarize(pf.describe().split(" kernels:")[0], pf, tm, "mfma", key="reference_profile_permute_conv3d")
+                    s["reference_m5_tflops"] = 9.07
+                    s["overhead_vs_dhwio_pct"] = 100.0 * (tm[0] / cfgs[key]["ms_per_step"] - 1.0)
+                    cfgs["reference_profile_permute_conv3d"] = s
             # OIDHW -> DHWIO weight re-layout at the reference's profile shape (512 x 512, 3x3x3;
             # AGENTS.md:51), HBM-bound: 40 rotating source copies (566 MB with the destination) so the
             # 256 MB Infinity Cache cannot serve the repeats

@@ -99,7 +99,7 @@ class ConvDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "rank", "N", "D", "H", "W", "C", "O", "KD", "KH", "KW", "stride_d", "stride_h", "stride_w",
         "dil_d", "dil_h", "dil_w", "pad_front", "pad_back", "pad_top", "pad_bottom", "pad_left", "pad_right",
-        "has_bias", "dtype")]
+        "has_bias", "dtype", "weight_layout")]
 
 
 class ConvArgs(ctypes.Structure):
@@ -487,10 +487,15 @@ def permute_oidhw_to_dhwio(dev: Device, w) -> np.ndarray:
     return out
 
 
-def conv_desc(dims, has_bias=False, rank=None) -> ConvDesc:
+WEIGHTS_DHWIO, WEIGHTS_OIDHW = 0, 1
+
+
+def conv_desc(dims, has_bias=False, rank=None, weight_layout="DHWIO") -> ConvDesc:
     """Descriptor from any object with the oracle's ConvDims field names (N, D, H, ..., PL, PR).
 
-    rank defaults to 2 when the depth axis is trivial (D = KD = 1, no depth padding), else 3."""
+    rank defaults to 2 when the depth axis is trivial (D = KD = 1, no depth padding), else 3.
+    weight_layout "OIDHW": the weights are [O][C][KD][KH][KW] and each run re-lays them out in the
+    plan's workspace first (the reference's PermuteThenTensorOpSession3D)."""
     g = (lambda k, dflt=0: getattr(dims, k, dflt))
     if rank is None:
         rank = 2 if (g("D", 1) == 1 and g("KD", 1) == 1 and not g("PF") and not g("PBk")) else 3
@@ -498,7 +503,8 @@ def conv_desc(dims, has_bias=False, rank=None) -> ConvDesc:
                     KH=g("KH"), KW=g("KW"), stride_d=g("SZ", 1), stride_h=g("SY", 1), stride_w=g("SX", 1),
                     dil_d=g("DZ", 1), dil_h=g("DY", 1), dil_w=g("DX", 1), pad_front=g("PF"), pad_back=g("PBk"),
                     pad_top=g("PT"), pad_bottom=g("PB"), pad_left=g("PL"), pad_right=g("PR"),
-                    has_bias=1 if has_bias else 0, dtype=F16)
+                    has_bias=1 if has_bias else 0, dtype=F16,
+                    weight_layout={"DHWIO": WEIGHTS_DHWIO, "OIDHW": WEIGHTS_OIDHW}[weight_layout])
 
 
 class ConvPlan(_Plan):
@@ -586,18 +592,21 @@ def attention_bwd(dev: Device, Q, K, V, O, dO, lse, *, causal=False, dtype="f16"
     return res
 
 
-def conv(dev: Device, dims, x, w, bias=None) -> np.ndarray:
-    """TensorOpSession*.run equivalent: one implicit-GEMM launch; returns the f16 output."""
-    desc = conv_desc(dims, has_bias=bias is not None)
+def conv(dev: Device, dims, x, w, bias=None, *, weight_layout="DHWIO") -> np.ndarray:
+    """TensorOpSession*.run equivalent: one implicit-GEMM launch; returns the f16 output. With
+    weight_layout "OIDHW", w is [O][C][KD][KH][KW] (rank 2: [O][C][KH][KW]) and the run re-lays it
+    out first (PermuteThenTensorOpSession3D.run)."""
+    desc = conv_desc(dims, has_bias=bias is not None, weight_layout=weight_layout)
     plan = ConvPlan(dev, desc)
     shape = plan.out_shape()
     dx, dw = dev.upload(_bits(x)), dev.upload(_bits(w))
     db = dev.upload(_bits(bias)) if bias is not None else None
     dy = dev.empty(int(np.prod(shape)) * 2)
-    plan.run(dx, dw, db, dy)
+    ws = dev.empty(plan.workspace_bytes) if plan.workspace_bytes else None
+    plan.run(dx, dw, db, dy, ws)
     dev.sync()
     out = dev.download(dy, shape, np.float16)
-    for b in (dx, dw, db, dy):
+    for b in (dx, dw, db, dy, ws):
         if b is not None:
             b.free()
     return out

@@ -85,7 +85,7 @@ namespace {
 
 enum PlanKind { PLAN_GEMM = 1, PLAN_ATTN = 2, PLAN_CONV = 3, PLAN_ATTN_BWD = 4, PLAN_PERMUTE = 5 };
 
-enum LaunchRole { ROLE_MAIN = 0, ROLE_REDUCE = 1 };
+enum LaunchRole { ROLE_MAIN = 0, ROLE_REDUCE = 1, ROLE_PERMUTE = 2 };
 
 struct Launch {
   std::string name;
@@ -519,6 +519,8 @@ int normalise_conv(const mtk_conv_desc *in, mtk_conv_desc *d) {
   if (d->pad_front < 0 || d->pad_back < 0 || d->pad_top < 0 || d->pad_bottom < 0 || d->pad_left < 0 || d->pad_right < 0)
     return fail(MTK_ERR_INVALID, "padding must be non-negative");
   if (d->dtype != MTK_F16) return fail(MTK_ERR_INVALID, "convolution dtype must be MTK_F16");
+  if (d->weight_layout != MTK_WEIGHTS_DHWIO && d->weight_layout != MTK_WEIGHTS_OIDHW)
+    return fail(MTK_ERR_INVALID, "weight_layout must be MTK_WEIGHTS_DHWIO or MTK_WEIGHTS_OIDHW (got %d)", d->weight_layout);
   int od, oh, ow;
   conv_out(d, &od, &oh, &ow);
   if (d->D + d->pad_front + d->pad_back < (d->KD - 1) * d->dil_d + 1 || d->H + d->pad_top + d->pad_bottom < (d->KH - 1) * d->dil_h + 1 ||
@@ -571,6 +573,26 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
   p->align_a = fast ? 16 : 2 * va;
   p->align_b = fast ? 4 : 2 * va;
   const char *kind = fast ? "fast" : "gen";
+  // OIDHW weights (the reference's PermuteThenTensorOpSession3D, ConvolutionShared.swift:1676-1857):
+  // the re-layout kernel writes DHWIO weights into the plan's workspace and the convolution reads
+  // them there, both in one run. The weights' own alignment is then the re-layout kernel's.
+  const bool oidhw = d.weight_layout == MTK_WEIGHTS_OIDHW;
+  if (oidhw) {
+    const long long ct = K;  // C * KD * KH * KW
+    const bool vec = ct % 8 == 0 && d.O % 8 == 0;
+    Launch pm;
+    pm.name = vec ? "mtk_permute_oidhw_dhwio_v8" : "mtk_permute_oidhw_dhwio_v1";
+    pm.grid = (unsigned)(((d.O + 63) / 64) * ((ct + 63) / 64));
+    pm.role = ROLE_PERMUTE;
+    mtk_permute_args pa{};
+    pa.O = d.O;
+    pa.C = d.C;
+    pa.T = d.KD * d.KH * d.KW;
+    set_args(pm, pa);
+    p->launches.push_back(pm);
+    p->align_b = vec ? 16 : 2;
+    p->workspace = ((size_t)w_bytes + 255) & ~(size_t)255;
+  }
   Launch g;
   char name[96];
   if (fast)
@@ -618,10 +640,11 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
   set_args(g, a);
   p->launches.push_back(g);
   p->flops = 2.0 * (double)M * d.O * (double)K;
-  p->bytes = (double)x_bytes + (double)w_bytes + 2.0 * (double)y_elems + (d.has_bias ? 2.0 * d.O : 0);
-  char desc[256];
-  snprintf(desc, sizeof desc, "conv%dd f16 implicit-GEMM M=%lld N=%d K=%lld out=%dx%dx%d tile=%dx%d gather=%s grid=%u",
-           d.rank, M, d.O, K, od, oh, ow, bm, bn, kind, g.grid);
+  p->bytes = (double)x_bytes + (double)w_bytes + 2.0 * (double)y_elems + (d.has_bias ? 2.0 * d.O : 0) +
+             (oidhw ? 2.0 * (double)w_bytes : 0.0);  // the re-layout reads and writes the weights once
+  char desc[288];
+  snprintf(desc, sizeof desc, "conv%dd f16 implicit-GEMM M=%lld N=%d K=%lld out=%dx%dx%d tile=%dx%d gather=%s grid=%u%s",
+           d.rank, M, d.O, K, od, oh, ow, bm, bn, kind, g.grid, oidhw ? " weights OIDHW (re-laid out in the workspace)" : "");
   p->description = desc;
   s = resolve(p);
   if (s != MTK_OK) {
@@ -771,12 +794,26 @@ int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
     if (p->conv.has_bias && !c->bias) return fail(MTK_ERR_INVALID, "plan has a bias but bias is null");
     if (!aligned(c->x, p->align_a) || !aligned(c->w, p->align_b))
       return fail(MTK_ERR_INVALID, "x must be %u-byte and w %u-byte aligned for this plan", p->align_a, p->align_b);
-    mtk_tile_args &a = args_of<mtk_tile_args>(ls[0]);
-    a.A = c->x;
-    a.B = c->w;
-    a.bias = c->bias;
-    a.C = c->y;
-    a.partial = nullptr;
+    if (p->workspace && (!c->workspace || !aligned(c->workspace, 16)))
+      return fail(MTK_ERR_INVALID, "this plan needs a 16-byte aligned workspace of %zu bytes", p->workspace);
+    if (p->workspace) {
+      const char *w0 = (const char *)c->w, *s0 = (const char *)c->workspace;
+      if (w0 < s0 + p->workspace && s0 < w0 + p->workspace) return fail(MTK_ERR_INVALID, "w and workspace overlap");
+    }
+    for (Launch &l : ls) {
+      if (l.role == ROLE_PERMUTE) {
+        mtk_permute_args &pa = args_of<mtk_permute_args>(l);
+        pa.src = c->w;
+        pa.dst = c->workspace;
+        continue;
+      }
+      mtk_tile_args &a = args_of<mtk_tile_args>(l);
+      a.A = c->x;
+      a.B = p->workspace ? c->workspace : c->w;
+      a.bias = c->bias;
+      a.C = c->y;
+      a.partial = nullptr;
+    }
   } else if (p->kind == PLAN_PERMUTE) {
     const mtk_permute_run_args *t = (const mtk_permute_run_args *)argset;
     if (!t || !t->src || !t->dst) return fail(MTK_ERR_INVALID, "src and dst must be non-null");

@@ -243,7 +243,14 @@ int mtk_attn_bwd_run(const mtk_plan *plan, const mtk_attn_bwd_args *args);
  * Cross-correlation with stride, dilation and zero padding; output size
  *   OH = (H + pad_top + pad_bottom - ((KH - 1) * dil_h + 1)) / stride_h + 1 (same for W, D).
  * Depth padding (pad_front/pad_back) extends the reference, which has none. bias [O] or NULL.
- * f16 only (the reference's conv path is f16). */
+ * f16 only (the reference's conv path is f16).
+ * weight_layout MTK_WEIGHTS_OIDHW: w is [O][C][KD][KH][KW] (rank 2: [O][C][KH][KW]), the layout of
+ * the reference's PermuteThenTensorOpSession3D (ConvolutionShared.swift:1676-1857): each run first
+ * re-lays the weights out to DHWIO in the caller's workspace (mtk_plan_workspace_bytes, the weight
+ * size rounded up to 256 bytes; it must not overlap w), then convolves from there, as the
+ * reference's session encodes the permutation and the convolution into one command buffer. */
+#define MTK_WEIGHTS_DHWIO 0
+#define MTK_WEIGHTS_OIDHW 1
 typedef struct {
   int rank; /* 2 or 3 */
   int N, D, H, W, C, O;
@@ -252,7 +259,8 @@ typedef struct {
   int dil_d, dil_h, dil_w;
   int pad_front, pad_back, pad_top, pad_bottom, pad_left, pad_right;
   int has_bias;
-  int dtype; /* MTK_F16 */
+  int dtype;         /* MTK_F16 */
+  int weight_layout; /* appended: MTK_WEIGHTS_DHWIO (0, the default) or MTK_WEIGHTS_OIDHW */
 } mtk_conv_desc;
 
 /* Replaces TensorOpSession / TensorOpSession3D / TensorOpBiasSession3D /

@@ -38,6 +38,72 @@ def test_permute_then_conv(dev):
     assert np.array_equal(y1.view(np.uint16), y0.view(np.uint16))
 
 
+def _oidhw(w):
+    """DHWIO [KD][KH][KW][C][O] (or HWIO) -> OIDHW [O][C][KD][KH][KW] (or OIHW), exact."""
+    return np.ascontiguousarray(np.transpose(w, (w.ndim - 1, w.ndim - 2) + tuple(range(w.ndim - 2))))
+
+
+@pytest.mark.parametrize("case", [
+    dict(rank=3, N=1, D=5, H=9, W=10, C=64, O=64, PF=1, PBk=1, PT=1, PB=1, PL=1, PR=1),  # fast gather
+    dict(rank=3, N=2, D=6, H=7, W=8, C=128, O=96, SZ=2, SY=1, SX=2, DY=2, PT=2, PB=2),  # strided, dilated
+    dict(rank=2, N=2, H=17, W=19, C=64, O=72, PT=1, PB=1, PL=1, PR=1),                 # OIHW, rank 2
+    dict(rank=3, N=1, D=4, H=6, W=7, C=24, O=20, PL=1, PR=1),                          # generic gather, 2-byte re-layout
+])
+@pytest.mark.parametrize("bias", [False, True])
+def test_oidhw_conv_plan(dev, case, bias):
+    # the reference's PermuteThenTensorOpSession3D (ConvolutionShared.swift:1676-1857) as one plan:
+    # each run re-lays the OIDHW weights out in the workspace and convolves from there; bit-exact
+    # against the oracle (integer generators: exact fp32 sums) and against permute-then-conv
+    case = dict(case)
+    rank = case.pop("rank")
+    d = (oracle.ConvDims.conv3d if rank == 3 else oracle.ConvDims.conv2d)(**case)
+    x, w = gen.conv3d_activation(d), gen.conv3d_weights(d)
+    b = gen.conv3d_bias(d) if bias else None
+    if rank == 2:
+        w = w.reshape(d.KH, d.KW, d.C, d.O)
+    print(f"[oidhw conv] rank {rank} {case} bias={bias}", flush=True)
+    y = mtk.conv(dev, d, x, _oidhw(w), b, weight_layout="OIDHW")
+    exp = oracle.conv(d, x, w.reshape(d.w_shape()), b).astype(np.float16).reshape(y.shape)
+    assert np.array_equal(y.view(np.uint16), exp.view(np.uint16))
+    y2 = mtk.conv(dev, d, x, mtk.permute_oidhw_to_dhwio(dev, _oidhw(w).reshape(d.O, d.C, d.KD, d.KH, d.KW)), b)
+    assert np.array_equal(y.view(np.uint16), y2.view(np.uint16))
+
+
+def test_oidhw_conv_reference_profile_shape(dev):
+    # the reference's permute + conv profile (AGENTS.md:49-53): N1 D3 256x256 C=O=512 3x3x3, no
+    # padding; integer generators (exact fp32 sums, |sum| <= 4158): the fused plan equals the
+    # DHWIO plan bit for bit and sampled output rows equal the oracle bit for bit
+    d = oracle.ConvDims.conv3d(N=1, D=3, H=256, W=256, C=512, O=512)
+    x, w = gen.conv3d_activation(d), gen.conv3d_weights(d)
+    y = mtk.conv(dev, d, x, _oidhw(w), weight_layout="OIDHW")
+    y0 = mtk.conv(dev, d, x, w)
+    assert np.array_equal(y.view(np.uint16), y0.view(np.uint16))
+    rows = y.reshape(-1, d.OW, d.O)
+    for r0 in (0, 101, 253):
+        exp = oracle.conv(d, x, w, rows=(r0, r0 + 1)).reshape(-1, d.OW, d.O)[r0]
+        assert np.array_equal(rows[r0].view(np.uint16), exp.astype(np.float16).view(np.uint16)), r0
+
+
+def test_oidhw_conv_errors(dev):
+    d = oracle.ConvDims.conv3d(N=1, D=3, H=8, W=8, C=64, O=64)
+    plan = mtk.ConvPlan(dev, mtk.conv_desc(d, weight_layout="OIDHW"))
+    assert plan.workspace_bytes == 64 * 64 * 27 * 2
+    x, w, y = dev.empty(3 * 8 * 8 * 64 * 2), dev.empty(64 * 64 * 27 * 2), dev.empty(6 * 6 * 64 * 2)
+    with pytest.raises(mtk.MtkError) as e:  # no workspace
+        plan.run(x, w, None, y)
+    assert e.value.status == mtk.MTK_ERR_INVALID
+    with pytest.raises(mtk.MtkError) as e:  # workspace overlapping the weights
+        plan.run(x, w, None, y, w.ptr + 256)
+    assert "overlap" in e.value.message
+    bad = mtk.conv_desc(d)
+    bad.weight_layout = 7
+    with pytest.raises(mtk.MtkError) as e:
+        mtk.ConvPlan(dev, bad)
+    assert e.value.status == mtk.MTK_ERR_INVALID
+    for b in (x, w, y):
+        b.free()
+
+
 def test_permute_errors(dev):
     with pytest.raises(mtk.MtkError) as e:
         mtk.PermutePlan(dev, 0, 4, 3, 3, 3)
