@@ -7,7 +7,8 @@
 
 using namespace mtk;
 
-// 256x256 tiles: 8 wavefronts (2 x 4, two per SIMD); smaller tiles: 4 (2 x 2).
+// 256x256 tiles: 8 wavefronts (2 x 4, two per SIMD, one workgroup per CU); 128x128: 4 (2 x 2, two
+// workgroups per CU).
 #define DIRECT_KERNEL(NAME, BM, BN, WM, WN)                                                          \
   extern "C" __global__ void __launch_bounds__(64 * WM * WN) NAME(const mtk_tile_args a) {        \
     tile_direct<DT_F16, BM, BN, WM, WN, OpConv<BM, WM * WN>, OpColsT<BN, WM * WN>>(a);            \
@@ -19,7 +20,6 @@ using namespace mtk;
   }
 
 DIRECT_KERNEL(mtk_conv_f16_fast_256x256_d, 256, 256, 2, 4)
-DIRECT_KERNEL(mtk_conv_f16_fast_256x128_d, 256, 128, 2, 2)
 DIRECT_KERNEL(mtk_conv_f16_fast_128x128_d, 128, 128, 2, 2)
 
 TILE_KERNEL(mtk_conv_f16_gen_128x128_v8, DT_F16, 128, 128, 2, 2, A_CONV_GENERIC, B_KN, 8, 8)

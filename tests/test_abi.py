@@ -46,7 +46,7 @@ def test_code_objects_hold_every_selectable_kernel():
     names += ["mtk_splitk_reduce_f16", "mtk_splitk_reduce_bf16", "mtk_fill_u16", "mtk_skinny_f16", "mtk_skinny_bf16",
               "mtk_skinny_f16_long", "mtk_skinny_bf16_long"]
     names += [f"mtk_attn_fwd_{w}{dt}{c}" for w in ("", "pp_") for dt in ("f16", "bf16") for c in ("", "_causal")]
-    names += [f"mtk_conv_f16_fast_{t}_d" for t in ("256x256", "256x128", "128x128")]
+    names += [f"mtk_conv_f16_fast_{t}_d" for t in ("256x256", "128x128")]
     names += [f"mtk_conv_f16_gen_128x128_v{v}" for v in (8, 4, 1)]
     missing = [n for n in names if n.encode() not in blobs]
     assert not missing, missing
@@ -227,7 +227,7 @@ def test_conv_kernel_select_and_shapes():
     assert p.work()[0] == d.flops() == 154618822656
     d3 = oracle.ConvDims.conv3d(N=1, D=16, H=64, W=64, C=128, O=128, PF=1, PBk=1, PT=1, PB=1, PL=1, PR=1)
     p = mtk.ConvPlan(None, mtk.conv_desc(d3))
-    assert "mtk_conv_f16_fast_256x128_d" in p.describe() and p.out_shape() == (1, 16, 64, 64, 128)
+    assert "mtk_conv_f16_fast_128x128_d" in p.describe() and p.out_shape() == (1, 16, 64, 64, 128)
     assert p.work()[0] == d3.flops() == 57982058496
     # the reference's case lists: every output shape agrees with the oracle's formulas
     import json
