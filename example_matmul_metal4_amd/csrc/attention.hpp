@@ -111,9 +111,12 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
   const int D = a.D;  // head dimension (<= DP)
 
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = id / a.q_blocks;
+  int bh = id / a.q_blocks;
   int qb = id - bh * a.q_blocks;
-  if (CAUSAL) qb = a.q_blocks - 1 - qb;  // heaviest query blocks first
+  if (CAUSAL) {  // heaviest (last) query blocks first
+    causal_order(id, a.q_blocks, a.B * a.H, bh, qb);
+    qb = a.q_blocks - 1 - qb;
+  }
   const int b = bh / a.H, h = bh - b * a.H;
   const int q0 = qb * kBQ;
   const uint32_t rs = (uint32_t)a.H * D * 2;      // bytes between sequence positions of Q / O

@@ -120,8 +120,9 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   const int g = lane >> 5, col = lane & 31;
 
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = id / a.k_blocks;  // (batch, K/V head)
-  const int kb = id - bh * a.k_blocks;
+  int bh = id / a.k_blocks;  // (batch, K/V head)
+  int kb = id - bh * a.k_blocks;
+  if (CAUSAL) causal_order(id, a.k_blocks, a.B * a.H_kv, bh, kb);  // heaviest (first) key blocks first
   const int b = bh / a.H_kv, hk = bh - b * a.H_kv;
   const int group = a.H / a.H_kv;  // query heads hk * group .. hk * group + group - 1
   const int k0 = kb * kBwdKeys;
@@ -314,9 +315,12 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
   const int g = lane >> 5, col = lane & 31;
 
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = id / a.q_blocks;
+  int bh = id / a.q_blocks;
   int qblk = id - bh * a.q_blocks;
-  if (CAUSAL) qblk = a.q_blocks - 1 - qblk;  // heaviest query blocks first
+  if (CAUSAL) {  // heaviest (last) query blocks first
+    causal_order(id, a.q_blocks, a.B * a.H, bh, qblk);
+    qblk = a.q_blocks - 1 - qblk;
+  }
   const int b = bh / a.H, h = bh - b * a.H;
   const int hk = h / (a.H / a.H_kv);  // K/V head of query head h
   const int q0 = qblk * kBwdQRows;

@@ -235,4 +235,24 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + (b >> 3);
 }
 
+// Causal attention grids: blocks of unequal work (query blocks near the end of the sequence see
+// more keys; key blocks near its start are seen by more queries). Workgroup id (after xcd_remap,
+// so an XCD holds a contiguous id range) -> (batch-head pair bh, rank), rank 0 = the pair's
+// heaviest block. Ids run over groups of kCausalGroup pairs, each group's blocks heaviest first
+// and interleaved across its pairs: each XCD then starts its longest blocks first (list
+// scheduling in that order balances the unequal blocks) while it works on the K/V of about
+// kCausalGroup pairs at a time (L2 reuse). With every pair's blocks heaviest first but pair after
+// pair, an XCD's last pairs started late and ran their longest blocks alone at the end.
+#ifndef MTK_CAUSAL_GROUP
+#define MTK_CAUSAL_GROUP 4
+#endif
+constexpr int kCausalGroup = MTK_CAUSAL_GROUP;
+__device__ __forceinline__ void causal_order(int id, int nblk, int nbh, int &bh, int &rank) {
+  const int g0 = (id / (kCausalGroup * nblk)) * kCausalGroup;
+  const int gn = min(kCausalGroup, nbh - g0);
+  const int r = id - g0 * nblk;
+  bh = g0 + r % gn;
+  rank = r / gn;
+}
+
 }  // namespace mtk
