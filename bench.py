@@ -348,6 +348,16 @@ def main():
                     s["reference_m5_tflops"] = 9.07
                     s["overhead_vs_dhwio_pct"] = 100.0 * (tm[0] / cfgs[key]["ms_per_step"] - 1.0)
                     cfgs["reference_profile_permute_conv3d"] = s
+                    # the permutation fused into the convolution's weight staging instead: the same
+                    # OIDHW weights read in place (one kernel, no workspace, 2-byte weight gathers)
+                    desc.weight_layout = mtk.WEIGHTS_OIDHW_DIRECT
+                    pd = mtk.ConvPlan(dev, desc)
+                    sets_d = [pd.args(sf.x, sf.w, None, y) for sf in sets_f]
+                    tm = time_steps(dev, pd, sets_d, args.warmup, steps)
+                    s = summarize(pd.describe().split(" kernels:")[0], pd, tm, "mfma",
+                                  key="reference_profile_oidhw_direct_conv3d")
+                    s["vs_two_pass_permute_conv"] = tm[0] / cfgs["reference_profile_permute_conv3d"]["ms_per_step"]
+                    cfgs["reference_profile_oidhw_direct_conv3d"] = s
             # OIDHW -> DHWIO weight re-layout at the reference's profile shape (512 x 512, 3x3x3;
             # AGENTS.md:51), HBM-bound: 40 rotating source copies (566 MB with the destination) so the
             # 256 MB Infinity Cache cannot serve the repeats

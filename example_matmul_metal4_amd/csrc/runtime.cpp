@@ -519,8 +519,11 @@ int normalise_conv(const mtk_conv_desc *in, mtk_conv_desc *d) {
   if (d->pad_front < 0 || d->pad_back < 0 || d->pad_top < 0 || d->pad_bottom < 0 || d->pad_left < 0 || d->pad_right < 0)
     return fail(MTK_ERR_INVALID, "padding must be non-negative");
   if (d->dtype != MTK_F16) return fail(MTK_ERR_INVALID, "convolution dtype must be MTK_F16");
-  if (d->weight_layout != MTK_WEIGHTS_DHWIO && d->weight_layout != MTK_WEIGHTS_OIDHW)
-    return fail(MTK_ERR_INVALID, "weight_layout must be MTK_WEIGHTS_DHWIO or MTK_WEIGHTS_OIDHW (got %d)", d->weight_layout);
+  if (d->weight_layout != MTK_WEIGHTS_DHWIO && d->weight_layout != MTK_WEIGHTS_OIDHW &&
+      d->weight_layout != MTK_WEIGHTS_OIDHW_DIRECT)
+    return fail(MTK_ERR_INVALID,
+                "weight_layout must be MTK_WEIGHTS_DHWIO, MTK_WEIGHTS_OIDHW or MTK_WEIGHTS_OIDHW_DIRECT (got %d)",
+                d->weight_layout);
   int od, oh, ow;
   conv_out(d, &od, &oh, &ow);
   if (d->D + d->pad_front + d->pad_back < (d->KD - 1) * d->dil_d + 1 || d->H + d->pad_top + d->pad_bottom < (d->KH - 1) * d->dil_h + 1 ||
@@ -551,7 +554,10 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
   // C % 64 == 0 (every 64-wide K-tile is one filter tap), even O and filter extents <= 10: the
   // direct-to-LDS pipeline (gather with padding as out-of-range loads, weights read transposed).
   // Anything else: the register-staged generic gather.
-  const bool fast = (d.C % 64) == 0 && d.O % 2 == 0 && d.KD <= 10 && d.KH <= 10 && d.KW <= 10;
+  // MTK_WEIGHTS_OIDHW_DIRECT: the register-staged kernel reads the OIDHW weights in place (no
+  // re-layout pass, no workspace; every weight element is a 2-byte load of its own).
+  const bool direct_oidhw = d.weight_layout == MTK_WEIGHTS_OIDHW_DIRECT;
+  const bool fast = !direct_oidhw && (d.C % 64) == 0 && d.O % 2 == 0 && d.KD <= 10 && d.KH <= 10 && d.KW <= 10;
   int va, bm, bn;
   if (fast) {
     va = 8;
@@ -567,11 +573,11 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
     }
     if ((M + bm - 1) / bm * ((d.O + bn - 1) / bn) < 128) bm = bn = 128;
   } else {
-    va = pow2_vec({d.C, d.O});
+    va = direct_oidhw ? pow2_vec({d.C}) : pow2_vec({d.C, d.O});
     bm = bn = 128;
   }
   p->align_a = fast ? 16 : 2 * va;
-  p->align_b = fast ? 4 : 2 * va;
+  p->align_b = fast ? 4 : direct_oidhw ? 2 : 2 * va;
   const char *kind = fast ? "fast" : "gen";
   // OIDHW weights (the reference's PermuteThenTensorOpSession3D, ConvolutionShared.swift:1676-1857):
   // the re-layout kernel writes DHWIO weights into the plan's workspace and the convolution reads
@@ -598,7 +604,7 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
   if (fast)
     snprintf(name, sizeof name, "mtk_conv_f16_fast_%dx%d_d", bm, bn);
   else
-    snprintf(name, sizeof name, "mtk_conv_f16_gen_%dx%d_v%d", bm, bn, va);
+    snprintf(name, sizeof name, "mtk_conv_f16_gen_%dx%d_v%d%s", bm, bn, va, direct_oidhw ? "_oidhw" : "");
   g.name = name;
   if (fast && bm == 256 && bn == 256) g.block = 512;  // 8 wavefronts
   mtk_tile_args a{};
@@ -644,7 +650,10 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
              (oidhw ? 2.0 * (double)w_bytes : 0.0);  // the re-layout reads and writes the weights once
   char desc[288];
   snprintf(desc, sizeof desc, "conv%dd f16 implicit-GEMM M=%lld N=%d K=%lld out=%dx%dx%d tile=%dx%d gather=%s grid=%u%s",
-           d.rank, M, d.O, K, od, oh, ow, bm, bn, kind, g.grid, oidhw ? " weights OIDHW (re-laid out in the workspace)" : "");
+           d.rank, M, d.O, K, od, oh, ow, bm, bn, kind, g.grid,
+           oidhw          ? " weights OIDHW (re-laid out in the workspace)"
+           : direct_oidhw ? " weights OIDHW (read in place)"
+                          : "");
   p->description = desc;
   s = resolve(p);
   if (s != MTK_OK) {

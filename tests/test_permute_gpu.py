@@ -48,9 +48,11 @@ def _oidhw(w):
     dict(rank=3, N=2, D=6, H=7, W=8, C=128, O=96, SZ=2, SY=1, SX=2, DY=2, PT=2, PB=2),  # strided, dilated
     dict(rank=2, N=2, H=17, W=19, C=64, O=72, PT=1, PB=1, PL=1, PR=1),                 # OIHW, rank 2
     dict(rank=3, N=1, D=4, H=6, W=7, C=24, O=20, PL=1, PR=1),                          # generic gather, 2-byte re-layout
+    dict(rank=2, N=1, H=11, W=9, C=3, O=10, PT=1, PB=1, PL=1, PR=1),                   # 2-byte activation loads
 ])
 @pytest.mark.parametrize("bias", [False, True])
-def test_oidhw_conv_plan(dev, case, bias):
+@pytest.mark.parametrize("layout", ["OIDHW", "OIDHW_DIRECT"])
+def test_oidhw_conv_plan(dev, case, bias, layout):
     # the reference's PermuteThenTensorOpSession3D (ConvolutionShared.swift:1676-1857) as one plan:
     # each run re-lays the OIDHW weights out in the workspace and convolves from there; bit-exact
     # against the oracle (integer generators: exact fp32 sums) and against permute-then-conv
@@ -61,12 +63,37 @@ def test_oidhw_conv_plan(dev, case, bias):
     b = gen.conv3d_bias(d) if bias else None
     if rank == 2:
         w = w.reshape(d.KH, d.KW, d.C, d.O)
-    print(f"[oidhw conv] rank {rank} {case} bias={bias}", flush=True)
-    y = mtk.conv(dev, d, x, _oidhw(w), b, weight_layout="OIDHW")
+    print(f"[oidhw conv] {layout} rank {rank} {case} bias={bias}", flush=True)
+    y = mtk.conv(dev, d, x, _oidhw(w), b, weight_layout=layout)
     exp = oracle.conv(d, x, w.reshape(d.w_shape()), b).astype(np.float16).reshape(y.shape)
     assert np.array_equal(y.view(np.uint16), exp.view(np.uint16))
     y2 = mtk.conv(dev, d, x, mtk.permute_oidhw_to_dhwio(dev, _oidhw(w).reshape(d.O, d.C, d.KD, d.KH, d.KW)), b)
     assert np.array_equal(y.view(np.uint16), y2.view(np.uint16))
+
+
+@pytest.mark.parametrize("case", [
+    dict(rank=3, N=1, D=5, H=9, W=10, C=64, O=64, PF=1, PBk=1, PT=1, PB=1, PL=1, PR=1),
+    dict(rank=2, N=2, H=13, W=15, C=128, O=256, PT=1, PB=1, PL=1, PR=1),
+    dict(rank=3, N=2, D=6, H=7, W=8, C=40, O=36, SZ=2, SX=2, DY=2, PT=2, PB=2),
+])
+def test_oidhw_direct_random_data(dev, case):
+    # the permutation fused into the weight staging: on seeded U[-1, 1) data (inexact sums) the
+    # in-place OIDHW read gives the re-layout plan's result bit for bit (same K order, same MFMA
+    # operands), which is the DHWIO convolution's
+    case = dict(case)
+    rank = case.pop("rank")
+    d = (oracle.ConvDims.conv3d if rank == 3 else oracle.ConvDims.conv2d)(**case)
+    rng = np.random.default_rng(5)
+    x = rng.uniform(-1, 1, d.x_shape()).astype(np.float16)
+    w = rng.uniform(-1, 1, d.w_shape()).astype(np.float16)
+    b = rng.uniform(-1, 1, (d.O,)).astype(np.float16)
+    wo = np.ascontiguousarray(np.transpose(w, (4, 3, 0, 1, 2)))  # [O][C][KD][KH][KW]
+    if rank == 2:
+        w, wo = w.reshape(d.KH, d.KW, d.C, d.O), wo.reshape(d.O, d.C, d.KH, d.KW)
+    print(f"[oidhw direct] rank {rank} {case}", flush=True)
+    y = mtk.conv(dev, d, x, wo, b, weight_layout="OIDHW_DIRECT")
+    assert np.array_equal(y.view(np.uint16), mtk.conv(dev, d, x, wo, b, weight_layout="OIDHW").view(np.uint16))
+    assert np.array_equal(y.view(np.uint16), mtk.conv(dev, d, x, w, b).view(np.uint16))
 
 
 def test_oidhw_conv_reference_profile_shape(dev):
@@ -78,6 +105,8 @@ def test_oidhw_conv_reference_profile_shape(dev):
     y = mtk.conv(dev, d, x, _oidhw(w), weight_layout="OIDHW")
     y0 = mtk.conv(dev, d, x, w)
     assert np.array_equal(y.view(np.uint16), y0.view(np.uint16))
+    y1 = mtk.conv(dev, d, x, _oidhw(w), weight_layout="OIDHW_DIRECT")  # permutation fused into the staging
+    assert np.array_equal(y1.view(np.uint16), y0.view(np.uint16))
     rows = y.reshape(-1, d.OW, d.O)
     for r0 in (0, 101, 253):
         exp = oracle.conv(d, x, w, rows=(r0, r0 + 1)).reshape(-1, d.OW, d.O)[r0]
@@ -95,6 +124,7 @@ def test_oidhw_conv_errors(dev):
     with pytest.raises(mtk.MtkError) as e:  # workspace overlapping the weights
         plan.run(x, w, None, y, w.ptr + 256)
     assert "overlap" in e.value.message
+    assert mtk.ConvPlan(dev, mtk.conv_desc(d, weight_layout="OIDHW_DIRECT")).workspace_bytes == 0
     bad = mtk.conv_desc(d)
     bad.weight_layout = 7
     with pytest.raises(mtk.MtkError) as e:
