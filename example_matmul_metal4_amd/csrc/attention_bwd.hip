@@ -210,8 +210,15 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
       }
     }
 
-    // P and dS; register r of block qb is query qt0 + 32 qb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8)
+    // P and dS; register r of block qb is query qt0 + 32 qb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8).
+    // Masks only where the tile needs them (this wave's keys past S_kv, queries past S_q, or keys
+    // past the causal diagonal of the tile's first query): elsewhere every element is kept, with
+    // the same bits.
+    const int wave_k_max = k0 + wave * 32 + 31;
+    const bool need_mask = wave_k_max >= a.S_kv || qt0 + kBwdQTile > a.S_q || (CAUSAL && wave_k_max > qt0 + diag);
     u32x4 pb[4], sb[4];
+    auto softmax_tile = [&](auto mask_c) {
+    constexpr bool MASK = decltype(mask_c)::value;
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
 #pragma unroll
@@ -235,7 +242,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
         for (int e = 0; e < 8; ++e) {
           const int r = 8 * half + e;
           const int qi = q + e;
-          const bool ok = key_ok && qi < a.S_q && (!CAUSAL || key <= qi + diag);
+          const bool ok = !MASK || (key_ok && qi < a.S_q && (!CAUSAL || key <= qi + diag));
           const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][r], c, -lse[e]));
           pv[e] = ok ? pe : 0.0f;
           sv[e] = ok ? pe * (p[qb][r] - dd[e]) * a.scale : 0.0f;
@@ -248,6 +255,11 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
         }
       }
     }
+    };
+    if (need_mask)
+      softmax_tile(std::true_type{});
+    else
+      softmax_tile(std::false_type{});
 
     // dV^T += dO^T . P and dK^T += Q^T . dS, d block by d block
 #pragma unroll
@@ -389,8 +401,13 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
       }
     }
 
-    // dS^T; register r of block kb is key j0 + 32 kb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8)
+    // dS^T; register r of block kb is key j0 + 32 kb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8). Masks
+    // only where the tile needs them (as in the dK/dV kernel).
+    const int wave_q0 = q0 + wave * 32;
+    const bool need_mask = wave_q0 + 31 >= a.S_q || j0 + kBwdKTile > a.S_kv || (CAUSAL && j0 + kBwdKTile - 1 > wave_q0 + diag);
     u32x4 sb[4];
+    auto softmax_tile = [&](auto mask_c) {
+    constexpr bool MASK = decltype(mask_c)::value;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -400,7 +417,7 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
         for (int e = 0; e < 8; ++e) {
           const int r = 8 * half + e;
           const int kj = j0 + 32 * kb + 16 * half + 8 * g + e;
-          const bool ok = q_ok && kj < a.S_kv && (!CAUSAL || kj <= qi + diag);
+          const bool ok = !MASK || (q_ok && kj < a.S_kv && (!CAUSAL || kj <= qi + diag));
           const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], c, -lse2));
           sv[e] = ok ? pe * (p[kb][r] - dterm) * a.scale : 0.0f;
         }
@@ -408,6 +425,11 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
         for (int e = 0; e < 4; ++e) sb[2 * kb + half][e] = pack2<DT>(sv[2 * e], sv[2 * e + 1]);
       }
     }
+    };
+    if (need_mask)
+      softmax_tile(std::true_type{});
+    else
+      softmax_tile(std::false_type{});
 
     // dQ^T += K^T . dS^T, d block by d block
 #pragma unroll
