@@ -428,7 +428,7 @@ class AttentionPlan(_Plan):
 class AttentionBwdPlan(_Plan):
     """dQ, dK, dV of the loss sum(dO * O) (Network.swift:313-402) from Q, K, V, the forward's O and
     lse, and dO; tensors [B][S][H][D] (K, V, dK, dV with H_kv heads), lse [B][H][S_q] fp32; needs a
-    workspace (the D vector)."""
+    workspace (two per-query row terms)."""
 
     _args_type = AttnBwdArgs
     _run_fn = "mtk_attn_bwd_run"

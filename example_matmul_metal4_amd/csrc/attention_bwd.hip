@@ -102,7 +102,11 @@ __device__ __forceinline__ void attn_bwd_pre(const mtk_attn_bwd_kargs &a) {
     const int h = (int)(row % a.H);
     const long long bq = row / a.H;
     const int q = (int)(bq % a.S_q), b = (int)(bq / a.S_q);
-    a.Dt[((size_t)b * a.H + h) * a.S_q + q] = s;
+    const size_t i = ((size_t)b * a.H + h) * a.S_q + q;
+    // the row terms of the other two kernels, scaled once per row: D * scale (dS = P (dP - D) scale
+    // = P (dP scale - D scale)) and the base-2 log-sum-exp (P = exp2(S scale log2e - lse log2e))
+    a.Dt[i] = s * a.scale;
+    a.Lt[i] = a.lse[i] * 1.4426950408889634f;
   }
 }
 
@@ -132,8 +136,8 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   const rsrc_t rg = make_rsrc(a.dO, a.q_bytes);
   const rsrc_t rk = make_rsrc(a.K, a.kv_bytes);
   const rsrc_t rv = make_rsrc(a.V, a.kv_bytes);
-  const uint32_t row_bytes = (uint32_t)a.B * a.H * a.S_q * 4u;  // lse and D: [B][H][S_q] fp32
-  const rsrc_t rl = make_rsrc(a.lse, row_bytes);
+  const uint32_t row_bytes = (uint32_t)a.B * a.H * a.S_q * 4u;  // row terms: [B][H][S_q] fp32
+  const rsrc_t rl = make_rsrc(a.Lt, row_bytes);
   const rsrc_t rd = make_rsrc(a.Dt, row_bytes);
   const int diag = a.S_kv - a.S_q;  // key j is visible to query i iff j <= i + diag (causal)
   const float c = a.scale_log2;
@@ -231,8 +235,8 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
           const f32x4 d0 = *(const f32x4 *)(d_t + qr), d1 = *(const f32x4 *)(d_t + qr + 4);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            lse[e] = l0[e] * 1.4426950408889634f;
-            lse[4 + e] = l1[e] * 1.4426950408889634f;
+            lse[e] = l0[e];
+            lse[4 + e] = l1[e];
             dd[e] = d0[e];
             dd[4 + e] = d1[e];
           }
@@ -245,7 +249,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
           const bool ok = !MASK || (key_ok && qi < a.S_q && (!CAUSAL || key <= qi + diag));
           const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][r], c, -lse[e]));
           pv[e] = ok ? pe : 0.0f;
-          sv[e] = ok ? pe * (p[qb][r] - dd[e]) * a.scale : 0.0f;
+          sv[e] = ok ? pe * __builtin_fmaf(p[qb][r], a.scale, -dd[e]) : 0.0f;
         }
         const int js = 2 * qb + half;
 #pragma unroll
@@ -357,8 +361,8 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
     gf[ds] = buf_load16(rg, off);
   }
   const size_t ridx = ((size_t)b * a.H + h) * a.S_q + (size_t)(q_ok ? qi : 0);
-  const float lse2 = q_ok ? a.lse[ridx] * 1.4426950408889634f : 0.0f;
-  const float dterm = q_ok ? a.Dt[ridx] : 0.0f;
+  const float lse2 = q_ok ? a.Lt[ridx] : 0.0f;   // base-2 lse
+  const float dterm = q_ok ? a.Dt[ridx] : 0.0f;  // D * scale
 
   int kv_end = a.S_kv;
   if (CAUSAL) kv_end = min(a.S_kv, q0 + kBwdQRows + diag);
@@ -419,7 +423,7 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
           const int kj = j0 + 32 * kb + 16 * half + 8 * g + e;
           const bool ok = !MASK || (q_ok && kj < a.S_kv && (!CAUSAL || kj <= qi + diag));
           const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], c, -lse2));
-          sv[e] = ok ? pe * (p[kb][r] - dterm) * a.scale : 0.0f;
+          sv[e] = ok ? pe * __builtin_fmaf(p[kb][r], a.scale, -dterm) : 0.0f;
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) sb[2 * kb + half][e] = pack2<DT>(sv[2 * e], sv[2 * e + 1]);

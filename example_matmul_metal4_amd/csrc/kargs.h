@@ -9,7 +9,7 @@
 
 #include <stdint.h>
 
-#define MTK_KARGS_VERSION 8
+#define MTK_KARGS_VERSION 9
 
 /* Tile-GEMM kernels: plain GEMM (A [M][K] . B, B either [N][K] or [K][N]) and
  * implicit-GEMM convolution (A = im2col of an NDHWC activation, B = DHWIO
@@ -97,7 +97,7 @@ typedef struct {
 typedef struct {
   const void *Q, *K, *V, *O, *dO;
   const float *lse; /* [B][H][S_q] from the forward */
-  float *Dt;        /* [B][H][S_q] workspace: rowsum(dO * O) */
+  float *Dt;        /* [B][H][S_q] workspace: rowsum(dO * O) * scale */
   void *dQ, *dK, *dV;
   int32_t B, H, S_q, S_kv;
   int32_t H_kv;     /* K/V heads (divides H); dK, dV sum over the H / H_kv query heads of a group */
@@ -107,6 +107,7 @@ typedef struct {
   float scale_log2; /* log2(e) / sqrt(D) */
   float scale;      /* 1 / sqrt(D) */
   uint32_t q_bytes, kv_bytes;
+  float *Lt; /* [B][H][S_q] workspace: lse * log2(e) (base-2 log-sum-exp) */
 } mtk_attn_bwd_kargs;
 
 /* Convolution weight re-layout OIDHW -> DHWIO (16-bit elements). */

@@ -422,7 +422,8 @@ int plan_attn_bwd(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
     set_args(*l, a);
     p->launches.push_back(*l);
   }
-  p->workspace = ((size_t)d.B * d.H * d.S_q * sizeof(float) + 255) & ~(size_t)255;
+  // workspace: the scaled D-term, then the base-2 lse, [B][H][S_q] fp32 each
+  p->workspace = 2 * (((size_t)d.B * d.H * d.S_q * sizeof(float) + 255) & ~(size_t)255);
   double pairs = (double)d.S_q * d.S_kv;
   if (d.causal) {
     pairs = 0;
@@ -852,6 +853,7 @@ int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
       a.dO = t->dO;
       a.lse = t->lse;
       a.Dt = (float *)t->workspace;
+      a.Lt = (float *)((char *)t->workspace + p->workspace / 2);
       a.dQ = t->dQ;
       a.dK = t->dK;
       a.dV = t->dV;

@@ -221,7 +221,7 @@ int mtk_attn_run(const mtk_plan *plan, const mtk_attn_args *args);
  *   dV = P^T dO, dK = dS^T Q, dQ = dS K.
  * Same descriptor as the forward (q_rows must be 0); same layouts; causal as in the forward. With
  * H_kv < H, dK and dV of a K/V head sum the contributions of its H / H_kv query heads. The plan
- * needs a workspace of mtk_plan_workspace_bytes (the D vector). Deterministic: no atomics. */
+ * needs a workspace of mtk_plan_workspace_bytes (two per-query row terms, D * scale and lse * log2(e), computed by its first kernel). Deterministic: no atomics. */
 int mtk_attn_bwd_plan(mtk_ctx *ctx, const mtk_attn_desc *desc, mtk_plan **out);
 
 typedef struct {

@@ -304,7 +304,7 @@ def test_attention_grouped_kv_heads_plan():
     assert p.work()[0] == mtk.AttentionPlan(None, 1, 8, 512, 512, 128).work()[0]
     b = mtk.AttentionBwdPlan(None, 2, 8, 512, 300, 128, H_kv=2)
     assert "grids=512/12/32" in b.describe()  # pre: 2*512*8/16, dkdv: 3 key blocks * 2 * 2, dq: 2 * 2 * 8
-    assert b.workspace_bytes == 2 * 8 * 512 * 4
+    assert b.workspace_bytes == 2 * (2 * 8 * 512 * 4)  # D * scale and the base-2 lse per query row
     for hkv in (3, -1, 16):
         for plan in (mtk.AttentionPlan, mtk.AttentionBwdPlan):
             with pytest.raises(mtk.MtkError) as e:
