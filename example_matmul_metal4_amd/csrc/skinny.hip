@@ -6,24 +6,36 @@
 //
 // Work decomposition
 //   * Workgroup = split_k wavefronts; wavefront w owns K partition w for every column group the
-//     workgroup processes. The grid is persistent (at most one workgroup per CU): workgroup b
-//     walks the 16-column groups b, b + grid, b + 2 grid, ...
+//     workgroup processes. The grid is persistent (at most one workgroup per CU) and balanced:
+//     workgroup b owns the contiguous columns [b * per, b * per + per), per = ceil(N / grid),
+//     walked in groups of 16.
 //   * 16x16x32 MFMA, lane (r = lane % 16, q = lane / 16). K step s of a partition covers 32
-//     columns of K; lane (r, q) supplies elements 8q .. 8q+7 of that step, of A row r and of
-//     B row (group column r). One load instruction therefore reads 64 contiguous bytes of each of
-//     16 rows.
-//   * A partition of up to kSkinnyResident K steps keeps its A fragments in registers for the
-//     whole kernel, so only B is streamed; longer partitions reload A per group (from L2).
-//   * The next group's B loads are issued before the current group's MFMAs (two register
-//     buffers), so every wavefront keeps a full group of loads in flight while it computes.
-//   * Per group, the partitions' fp32 16x16 results meet in LDS (double buffered: one barrier
-//     per group); the workgroup sums partitions 0, 1, ... in order, adds the bias and stores.
+//     elements of K; lane (r, q) supplies elements 8q .. 8q+7 of that step, of A row r and of
+//     B row (group column r), i.e. chunk 4s + q (8 elements) of the partition.
+//   * Resident kernel (partitions of up to kSkinnyResident K steps): loads read whole cache lines.
+//     Load instruction s reads row s of the group (or of A), 16 bytes per lane: chunk `lane` of
+//     the partition, 1 KB contiguous per instruction. (Reading operand fragments directly, 64
+//     bytes of each of 16 rows per instruction, streams B at ~4.4 TB/s against ~6.3 TB/s here.)
+//     The wavefront transposes the 16 rows x 64 chunks through its own LDS region into fragment
+//     layout: row s chunk c is parked in slot c ^ s, so both the parking writes and the fragment
+//     reads of 16 lanes touch 16 distinct 16-byte bank groups. A is transposed once and kept in
+//     registers; B loads are non-temporal (streamed once), the next group's issued before the
+//     current group's MFMAs (two register buffers).
+//   * Per group the partitions' fp32 16x16 results are parked in an LDS slot; every kSkinnySlots
+//     groups (and after the last) the workgroup sums partitions 0, 1, ... in order, adds the bias
+//     and stores: one barrier pair per kSkinnySlots groups instead of one barrier per group.
+//   * The long kernel (longer partitions) loads fragments directly and reloads A per pass of
+//     kSkinnyResident steps (L2-resident: A is M x K).
 //   * Raw buffer loads: rows m >= M, columns n >= N and K past the partition read zero.
+//   The arithmetic of every output is the same in both kernels and for any grid: per partition a
+//   chain of MFMAs over its K steps in order from zero, partition sums added in partition order,
+//   the bias last.
 #include "device.hpp"
 
 namespace mtk {
 
 constexpr int kSkinnyResident = 16;  // K steps (x 32) a partition may keep resident: 512 K
+constexpr int kSkinnySlots = 2;      // column groups parked in LDS between reductions
 
 template <int DT, int KS>
 struct SkinnyWave {
@@ -71,8 +83,96 @@ __device__ __forceinline__ void skinny_reduce_store(const mtk_skinny_args &p, fl
   }
 }
 
-template <int DT, bool RESIDENT>
-__device__ __forceinline__ void skinny_gemm(const mtk_skinny_args &p) {
+// Resident partitions (K per partition <= 32 * kSkinnyResident): whole-line loads transposed
+// through LDS, balanced contiguous columns, reductions every kSkinnySlots groups.
+template <int DT>
+__device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
+  constexpr int KS = kSkinnyResident, R = kSkinnySlots;
+  // non-temporal B loads: each element of B is read once
+  constexpr int kStreamPolicy = 2;
+  __shared__ __attribute__((aligned(16))) float red[R][8][256];
+  __shared__ __attribute__((aligned(16))) u32x4 tr[8][KS][64];  // per wavefront: 16 rows x 64 chunks
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int per = (p.N + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int c0 = (int)blockIdx.x * per, c1 = min(p.N, c0 + per);
+  const int ng = c1 > c0 ? (c1 - c0 + 15) / 16 : 0;  // workgroup-uniform
+  const rsrc_t ra = make_rsrc(p.A, p.a_bytes);
+  const rsrc_t rb = make_rsrc(p.B, p.b_bytes);
+  const int k0 = w * p.k_per_split;
+  const int k_end = min(p.K, k0 + p.k_per_split);
+  const int kl = k0 + 8 * lane;  // the chunk this lane loads of every row
+  const bool k_ok = kl < k_end;
+  const int r = lane & 15, q = lane >> 4;
+  u32x4(&t)[KS][64] = tr[w];
+
+  // A: row s (s < M) -> slot lane ^ s, fragments read back once
+  u32x4 a[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+    a[s] = buf_load16(ra, (k_ok && s < p.M) ? (uint32_t)s * (uint32_t)p.lda * 2u + (uint32_t)kl * 2u : kOOB);
+#pragma unroll
+  for (int s = 0; s < KS; ++s) t[s][lane ^ s] = a[s];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) a[s] = t[r][(4 * s + q) ^ r];
+
+  auto load_b = [&](u32x4 (&b)[KS], int col) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int n = col + s;
+      b[s] = __builtin_amdgcn_raw_buffer_load_b128(
+          rb, (k_ok && n < c1) ? (uint32_t)n * (uint32_t)p.ldb * 2u + (uint32_t)kl * 2u : kOOB, 0, kStreamPolicy);
+    }
+  };
+  // LDS operations of one wavefront execute in order: the parking writes of a group follow the
+  // fragment reads of the previous one.
+  auto mma = [&](const u32x4 (&b)[KS]) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) t[s][lane ^ s] = b[s];
+    f32x4 acc{};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) acc = mfma16x16x32<DT>(a[s], t[r][(4 * s + q) ^ r], acc);
+    return acc;
+  };
+  // 16x16 accumulator layout: lane (c = lane % 16, g = lane / 16), register i -> row 4g + i, col c.
+  auto park = [&](int slot, f32x4 acc) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[slot][w][(4 * q + i) * 16 + r] = acc[i];
+  };
+  // groups g0 .. g0 + n - 1 are parked in slots 0 .. n - 1
+  auto flush = [&](int g0, int n) {
+    __syncthreads();
+    for (int e = tid; e < n * 256; e += (int)blockDim.x) {
+      const int sl = e >> 8, o = e & 255, m = o >> 4;
+      const int col = c0 + 16 * (g0 + sl) + (o & 15);
+      float sum = red[sl][0][o];
+      for (int ww = 1; ww < p.split_k; ++ww) sum += red[sl][ww][o];
+      if (m < p.M && col < c1) {
+        if (p.has_bias) sum += from_bits<DT>(((const uint16_t *)p.bias)[col]);
+        ((uint16_t *)p.C)[(size_t)m * p.ldc + col] = to_bits<DT>(sum);
+      }
+    }
+    __syncthreads();
+  };
+
+  u32x4 b0[KS], b1[KS];
+  if (ng > 0) load_b(b0, c0);
+  for (int g = 0; g < ng; g += 2) {
+    if (g + 1 < ng) load_b(b1, c0 + 16 * (g + 1));
+    park(g % R, mma(b0));
+    if (g % R == R - 1 || g + 1 == ng) flush(g - g % R, g % R + 1);
+    if (g + 1 >= ng) break;
+    if (g + 2 < ng) load_b(b0, c0 + 16 * (g + 2));
+    park((g + 1) % R, mma(b1));
+    if ((g + 1) % R == R - 1 || g + 2 == ng) flush(g + 1 - (g + 1) % R, (g + 1) % R + 1);
+  }
+}
+
+// Long partitions: passes of KS steps with fragments loaded directly and A reloaded per pass
+// (L2-resident: A is M x K); groups b, b + grid, ...; one reduction per group.
+template <int DT>
+__device__ __forceinline__ void skinny_gemm_long(const mtk_skinny_args &p) {
   // two LDS buffers of [partition][16 x 16] fp32
   __shared__ __attribute__((aligned(16))) float red[2][8][256];
 
@@ -88,50 +188,23 @@ __device__ __forceinline__ void skinny_gemm(const mtk_skinny_args &p) {
   sw.k0 = (uint32_t)(w * p.k_per_split);
   sw.k_end = (uint32_t)min(p.K, (int)sw.k0 + p.k_per_split);
 
-  // 16x16 accumulator layout: lane (c = lane % 16, g = lane / 16), register r -> row 4g + r, col c.
   auto park = [&](int buf, f32x4 acc) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[buf][w][(4 * (lane >> 4) + r) * 16 + (lane & 15)] = acc[r];
   };
-
-  if constexpr (RESIDENT) {
-    // the partition fits in KS steps: A stays in registers, B double-buffered across groups
-    sw.load_a(ra, (int)sw.k0, lane);
-    u32x4 b0[KS], b1[KS];
-    int g = blockIdx.x;
-    if (g < groups) sw.load_b(rb, b0, g, p.N, p.ldb, (int)sw.k0, lane);
-    int buf = 0;
-    for (; g < groups; g += 2 * gridDim.x) {
-      const int g1 = g + gridDim.x;
-      if (g1 < groups) sw.load_b(rb, b1, g1, p.N, p.ldb, (int)sw.k0, lane);
-      park(buf, sw.mma(b0, f32x4{}));
-      __syncthreads();
-      skinny_reduce_store<DT>(p, red[buf], g, tid);
-      buf ^= 1;
-      if (g1 >= groups) break;
-      const int g2 = g1 + gridDim.x;
-      if (g2 < groups) sw.load_b(rb, b0, g2, p.N, p.ldb, (int)sw.k0, lane);
-      park(buf, sw.mma(b1, f32x4{}));
-      __syncthreads();
-      skinny_reduce_store<DT>(p, red[buf], g1, tid);
-      buf ^= 1;
+  int buf = 0;
+  for (int g = blockIdx.x; g < groups; g += gridDim.x) {
+    f32x4 acc = f32x4{};
+    u32x4 b[KS];
+    for (int kb = (int)sw.k0; kb < (int)sw.k_end; kb += 32 * KS) {
+      sw.load_a(ra, kb, lane);
+      sw.load_b(rb, b, g, p.N, p.ldb, kb, lane);
+      acc = sw.mma(b, acc);
     }
-  } else {
-    // long partitions: passes of KS steps, A reloaded per pass (L2-resident: A is M x K)
-    int buf = 0;
-    for (int g = blockIdx.x; g < groups; g += gridDim.x) {
-      f32x4 acc = f32x4{};
-      u32x4 b[KS];
-      for (int kb = (int)sw.k0; kb < (int)sw.k_end; kb += 32 * KS) {
-        sw.load_a(ra, kb, lane);
-        sw.load_b(rb, b, g, p.N, p.ldb, kb, lane);
-        acc = sw.mma(b, acc);
-      }
-      park(buf, acc);
-      __syncthreads();
-      skinny_reduce_store<DT>(p, red[buf], g, tid);
-      buf ^= 1;
-    }
+    park(buf, acc);
+    __syncthreads();
+    skinny_reduce_store<DT>(p, red[buf], g, tid);
+    buf ^= 1;
   }
 }
 
@@ -139,10 +212,10 @@ __device__ __forceinline__ void skinny_gemm(const mtk_skinny_args &p) {
 
 using namespace mtk;
 
-#define SKINNY(NAME, DT, RES) \
-  extern "C" __global__ void __launch_bounds__(512) NAME(const mtk_skinny_args a) { skinny_gemm<DT, RES>(a); }
+#define SKINNY(NAME, DT, BODY) \
+  extern "C" __global__ void __launch_bounds__(512) NAME(const mtk_skinny_args a) { BODY<DT>(a); }
 
-SKINNY(mtk_skinny_f16, DT_F16, true)
-SKINNY(mtk_skinny_bf16, DT_BF16, true)
-SKINNY(mtk_skinny_f16_long, DT_F16, false)
-SKINNY(mtk_skinny_bf16_long, DT_BF16, false)
+SKINNY(mtk_skinny_f16, DT_F16, skinny_gemm_resident)
+SKINNY(mtk_skinny_bf16, DT_BF16, skinny_gemm_resident)
+SKINNY(mtk_skinny_f16_long, DT_F16, skinny_gemm_long)
+SKINNY(mtk_skinny_bf16_long, DT_BF16, skinny_gemm_long)

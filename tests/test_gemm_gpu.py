@@ -315,7 +315,10 @@ def test_config3_decode_skinny_full_size(dev):
     (1, 4096, 4096, 8, "bf16"), (3, 100, 1000, 3, "f16"), (16, 64, 128, 1, "f16"), (7, 333, 2048, 2, "bf16"),
     (16, 14336, 4096, 4, "f16"), (16, 48, 4104, 8, "f16"),
     # persistent grid: more 16-column groups than workgroups, odd and even counts per workgroup
-    (5, 8211, 512, 1, "f16"), (2, 9000, 2048, 1, "bf16")])
+    (5, 8211, 512, 1, "f16"), (2, 9000, 2048, 1, "bf16"),
+    # many column groups per workgroup (several LDS reductions each); partitions shorter than
+    # the 512 elements one load instruction covers
+    (16, 60000, 256, 2, "bf16"), (4, 4097, 1024, 8, "f16")])
 def test_skinny_shapes(dev, M, N, K, split_k, dtype):
     A = oracle.normal(20 + M, (M, K), 0, 1, dtype)
     B = oracle.normal(30 + M, (N, K), 0, 0.05, dtype)
