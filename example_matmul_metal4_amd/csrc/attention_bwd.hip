@@ -62,6 +62,20 @@ __device__ __forceinline__ u32x4 tr_frag(uint32_t base) {
   return u32x4{w0.x, w0.y, w1.x, w1.y};
 }
 
+#ifndef MTK_BWD_SDP_AHEAD
+#define MTK_BWD_SDP_AHEAD 8
+#endif
+#ifndef MTK_BWD_TR_AHEAD
+#define MTK_BWD_TR_AHEAD 8
+#endif
+// Wait until at most N LDS operations are outstanding; f (filled by an inline-asm read) is handed
+// on through the wait, so its consumers cannot be scheduled above it.
+template <int N>
+__device__ __forceinline__ void lgkm_wait_n(u32x4 &f) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(f) : "n"(N));
+}
+
 // Stage rows [row0, row0 + 4 * n) of a 64-row operand tile: instruction i fills 4 rows (1 KB),
 // lane l writes row row0 + 4 i + l / 16, LDS chunk l % 16, which holds global chunk
 // (l % 16) ^ swizzle(row). Rows at or past `rows_valid` read zero.
@@ -200,18 +214,37 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     const float *lse_t = (const float *)(st + 4 * kRowTile), *d_t = (const float *)(st + 4 * kRowTile + 1024);
     const int qt0 = (t0 + i % per_head) * kBwdQTile;
 
-    // S and dP for the two 32-query blocks of the tile
+    // S and dP for the two 32-query blocks of the tile: 32 MFMAs in four interleaved accumulation
+    // chains (step k: d step k / 4; S of block 0, dP of block 0, S of block 1, dP of block 1), each
+    // operand fragment read MTK_BWD_SDP_AHEAD steps ahead of its MFMA. The fence per step keeps
+    // that order (the scheduler would otherwise regroup the chains and read each fragment just
+    // before its use); every chain still accumulates its d steps in order.
     f32x16 s[2], p[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       s[qb] = f32x16{};
       p[qb] = f32x16{};
+    }
+    {
+      constexpr int D = MTK_BWD_SDP_AHEAD;
+      auto rd = [&](int k) {
+        const int ds = k >> 2, qb = (k >> 1) & 1;
+        return *(const u32x4 *)(((k & 1) ? grow : qrow) + row_off(32 * qb + arow, 2 * ds + g));
+      };
+      u32x4 fr[D];
 #pragma unroll
-      for (int ds = 0; ds < 8; ++ds) {
-        const uint32_t o = row_off(32 * qb + arow, 2 * ds + g);
-        s[qb] = mfma32x32x16<DT>(*(const u32x4 *)(qrow + o), kf[ds], s[qb]);
-        p[qb] = mfma32x32x16<DT>(*(const u32x4 *)(grow + o), vf[ds], p[qb]);
+      for (int k = 0; k < D; ++k) fr[k] = rd(k);
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int ds = k >> 2, qb = (k >> 1) & 1;
+        if (k & 1)
+          p[qb] = mfma32x32x16<DT>(fr[k % D], vf[ds], p[qb]);
+        else
+          s[qb] = mfma32x32x16<DT>(fr[k % D], kf[ds], s[qb]);
+        if (k + D < 32) fr[k % D] = rd(k + D);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
 
     // P and dS; register r of block qb is query qt0 + 32 qb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8).
@@ -265,23 +298,37 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     else
       softmax_tile(std::false_type{});
 
-    // dV^T += dO^T . P and dK^T += Q^T . dS, d block by d block
+    // dV^T += dO^T . P and dK^T += Q^T . dS: 32 MFMAs in eight interleaved accumulation chains
+    // (step k: 16-query step js = k / 8, d block (k / 2) % 4, dV for even k, dK for odd k), each
+    // transposed operand fragment read MTK_BWD_TR_AHEAD steps ahead; every dV[db] / dK[db] still
+    // accumulates js = 0..3 in order.
+    {
+      constexpr int D = MTK_BWD_TR_AHEAD;
+      uint32_t tb[8];
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const uint32_t gbase = tr_base(gtr, db, lane), qbase_ = tr_base(qtr, db, lane);
-      u32x4 gf[4], qf[4];
-      static_for<0, 4>([&](auto jc) {
-        constexpr int JS = decltype(jc)::value;
-        gf[JS] = tr_frag<JS>(gbase);
-        qf[JS] = tr_frag<JS>(qbase_);
-      });
-      lgkm_wait0(gf);
-      lgkm_wait0(qf);
-#pragma unroll
-      for (int js = 0; js < 4; ++js) {
-        dv[db] = mfma32x32x16<DT>(gf[js], pb[js], dv[db]);
-        dk[db] = mfma32x32x16<DT>(qf[js], sb[js], dk[db]);
+      for (int db = 0; db < 4; ++db) {
+        tb[2 * db] = tr_base(gtr, db, lane);
+        tb[2 * db + 1] = tr_base(qtr, db, lane);
       }
+      u32x4 tf[D];
+      auto rd = [&](auto kc) {
+        constexpr int K = decltype(kc)::value;
+        tf[K % D] = tr_frag<K / 8>(tb[K & 7]);
+      };
+      static_for<0, D>([&](auto kc) { rd(kc); });
+      static_for<0, 32>([&](auto kc) {
+        constexpr int K = decltype(kc)::value;
+        constexpr int kAfter = (31 - K) < (D - 1) ? (31 - K) : (D - 1);  // fragments read after K
+        __builtin_amdgcn_sched_barrier(0);
+        lgkm_wait_n<2 * kAfter>(tf[K % D]);
+        constexpr int js = K / 8, db = (K >> 1) & 3;
+        if constexpr (K & 1)
+          dk[db] = mfma32x32x16<DT>(tf[K % D], sb[js], dk[db]);
+        else
+          dv[db] = mfma32x32x16<DT>(tf[K % D], pb[js], dv[db]);
+        if constexpr (K + D < 32) rd(std::integral_constant<int, K + D>{});
+      });
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
