@@ -61,7 +61,8 @@ typedef struct {
   uint32_t v;
 } mtk_fill_args;
 
-/* Skinny (decode-shaped) GEMM: A [M <= 16][lda], B [N][ldb] (NK), fp32 partials per K split. */
+/* Skinny (decode-shaped) GEMM: A [M <= 16][lda] (M <= 32 for the partial-writing kernel), B [N][ldb] (NK);
+   partial: that kernel's output, [split_k][M][N] fp32. */
 typedef struct {
   const void *A;
   const void *B;

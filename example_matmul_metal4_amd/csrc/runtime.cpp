@@ -258,6 +258,70 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
     return MTK_OK;
   }
 
+  // 16 < M <= 32 with long K (the reference's default run, 32 x 3072 x 80000, split-K 30): B
+  // streamed once by the partial-writing skinny kernel, one workgroup per (K partition, 64
+  // columns), then the two-pass reduce. Same partition layout as the two-pass tile schedule
+  // (uniform partitions of whole 64-element K-tiles); needs split_k >= 2 after the plan's choice.
+  if (d.M > 16 && d.M <= 32 && !d.trans_a && d.trans_b && d.tile == 0 && d.split_mode != MTK_SPLIT_SERIAL &&
+      d.K >= 2048 && d.K % 8 == 0 && d.lda % 8 == 0 && d.ldb % 8 == 0) {
+    const int cus = ctx ? ctx->prop.multiProcessorCount : 256;
+    const long long ncb = (d.N + 63) / 64;
+    int split = d.split_k;
+    if (split == 0)  // about four workgroups per CU, partitions of at least 8 K-tiles
+      split = (int)std::min<long long>(std::max<long long>(2, (4LL * cus + ncb - 1) / ncb), std::max(1, k_tiles / 8));
+    split = std::min(split, k_tiles);
+    const int kps = (k_tiles + split - 1) / split;
+    split = (k_tiles + kps - 1) / kps;
+    if (split >= 2) {
+      Launch g;
+      g.name = std::string("mtk_skinny_parts_") + dt;
+      g.grid = (unsigned)(ncb * split);
+      g.block = 256;
+      mtk_skinny_args a{};
+      a.M = d.M;
+      a.N = d.N;
+      a.K = d.K;
+      a.lda = d.lda;
+      a.ldb = d.ldb;
+      a.ldc = d.ldc;
+      a.a_bytes = (uint32_t)a_bytes;
+      a.b_bytes = (uint32_t)b_bytes;
+      a.split_k = split;
+      a.k_per_split = kps * 64;
+      a.has_bias = d.has_bias ? 1 : 0;
+      set_args(g, a);
+      p->launches.push_back(g);
+      p->workspace = (size_t)split * d.M * d.N * sizeof(float);
+      Launch r;
+      r.role = ROLE_REDUCE;
+      r.name = std::string("mtk_splitk_reduce_") + dt;
+      mtk_reduce_args ra{};
+      ra.M = d.M;
+      ra.N = d.N;
+      ra.ldc = d.ldc;
+      ra.split_k = split;
+      ra.has_bias = a.has_bias;
+      ra.vec4 = (d.N % 4 == 0 && d.ldc % 4 == 0) ? 1 : 0;
+      const long long work = ra.vec4 ? (long long)d.M * d.N / 4 : (long long)d.M * d.N;
+      r.grid = (unsigned)std::min<long long>((work + 255) / 256, 65535);
+      set_args(r, ra);
+      p->launches.push_back(r);
+      p->align_a = p->align_b = 16;
+      char desc[256];
+      snprintf(desc, sizeof desc,
+               "gemm %s skinny partials M=%d N=%d K=%d split_k=%d k_tiles/split=%d grid=%u block=256 + splitk_reduce", dt,
+               d.M, d.N, d.K, split, kps, g.grid);
+      p->description = desc;
+      int st = resolve(p);
+      if (st != MTK_OK) {
+        delete p;
+        return st;
+      }
+      *out = p;
+      return MTK_OK;
+    }
+  }
+
   int tile = d.tile;
   int split = d.split_k;
   if (tile == 0) {
@@ -770,6 +834,7 @@ void patch_gemm(const mtk_plan *p, const Launch &l, char *block, const mtk_gemm_
     k->B = g->B;
     k->bias = g->bias;
     k->C = g->C;
+    k->partial = p->workspace ? (float *)ws : nullptr;  // the partial-writing kernel's output
     return;
   }
   const bool two_pass = p->workspace != 0 && !p->serial_split;

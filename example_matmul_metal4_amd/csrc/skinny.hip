@@ -208,6 +208,106 @@ __device__ __forceinline__ void skinny_gemm_long(const mtk_skinny_args &p) {
   }
 }
 
+// Partial-writing kernel for 16 < M <= 32 and long K, the shape of the reference's default run
+// (f16 32 x 3072 x 80000, split-K 30; matmul.swift main()): one workgroup per (K partition,
+// 64 columns), four wavefronts of 16 columns. It writes the two-pass schedule's fp32 partials
+// [split_k][M][N] (uniform partitions of k_per_split elements); the reduce kernel then adds them in
+// partition order and the bias. Per 512-element chunk of the partition:
+//   * A's 32 rows are staged once for the workgroup (direct-to-LDS, double buffered; lane l of
+//     row m loads chunk l ^ (m & 15), the slot it lands in is l), each wavefront loading 8 rows;
+//   * B's 16 rows of each wavefront are read 1 KB of one row per instruction (whole cache lines,
+//     non-temporal, double buffered in registers) and transposed through the wavefront's own LDS
+//     region as in the decode kernel;
+//   * 16 K steps of two 16x16x32 MFMAs (rows 0-15 and 16-31 of A) on one B fragment each.
+// Rows m >= M, columns n >= N and K past the partition read zero.
+template <int DT>
+__device__ __forceinline__ void skinny_gemm_parts(const mtk_skinny_args &p) {
+  constexpr int KS = kSkinnyResident;  // 16 K steps of 32: 512 elements per chunk
+  constexpr int kStreamPolicy = 2;     // non-temporal B loads
+  __shared__ __attribute__((aligned(1024))) u32x4 abuf[2][32][64];  // A chunk: 32 rows x 1 KB
+  __shared__ __attribute__((aligned(16))) u32x4 tr[4][KS][64];      // per wavefront: 16 rows x 1 KB
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int ncb = (p.N + 63) / 64;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);  // consecutive ids (the column blocks of one
+  const int part = id / ncb, cb = id - part * ncb;   // partition) share an XCD and its A
+  const int k0 = part * p.k_per_split;
+  const int k1 = min(p.K, k0 + p.k_per_split);
+  const int nch = k1 > k0 ? (k1 - k0 + 32 * KS - 1) / (32 * KS) : 0;
+  const int n0 = cb * 64 + 16 * w;  // this wavefront's first column
+  const rsrc_t ra = make_rsrc(p.A, p.a_bytes);
+  const rsrc_t rb = make_rsrc(p.B, p.b_bytes);
+  const int r = lane & 15, q = lane >> 4;
+  u32x4(&t)[KS][64] = tr[w];
+
+  auto load_a = [&](int buf, int kc) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int m = 8 * w + i;
+      const int k = kc + 8 * (lane ^ (m & 15));
+      lds_direct16(ra, (char *)&abuf[buf][m][0],
+                   (m < p.M && k < k1) ? (uint32_t)m * (uint32_t)p.lda * 2u + (uint32_t)k * 2u : kOOB);
+    }
+  };
+  auto load_b = [&](u32x4 (&b)[KS], int kc) {
+    const int k = kc + 8 * lane;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int n = n0 + s;
+      b[s] = __builtin_amdgcn_raw_buffer_load_b128(
+          rb, (n < p.N && k < k1) ? (uint32_t)n * (uint32_t)p.ldb * 2u + (uint32_t)k * 2u : kOOB, 0, kStreamPolicy);
+    }
+  };
+  f32x4 acc[2] = {f32x4{}, f32x4{}};
+  // chunk j: B fragments through this wavefront's LDS region, A fragments from the shared chunk
+  auto mma = [&](const u32x4 (&b)[KS], int buf) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) t[s][lane ^ s] = b[s];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const u32x4 bf = t[r][(4 * s + q) ^ r];
+#pragma unroll
+      for (int rb2 = 0; rb2 < 2; ++rb2) acc[rb2] = mfma16x16x32<DT>(abuf[buf][16 * rb2 + r][(4 * s + q) ^ r], bf, acc[rb2]);
+    }
+  };
+
+  u32x4 b0[KS], b1[KS];
+  if (nch > 0) {
+    load_a(0, k0);
+    load_b(b0, k0);
+  }
+  for (int j = 0; j < nch; j += 2) {
+    // chunk j (A in buffer 0, B in b0) has landed; every wavefront is done with buffer 1
+    wait_vmem();
+    __syncthreads();
+    if (j + 1 < nch) {
+      load_a(1, k0 + 32 * KS * (j + 1));
+      load_b(b1, k0 + 32 * KS * (j + 1));
+    }
+    mma(b0, 0);
+    if (j + 1 >= nch) break;
+    wait_vmem();
+    __syncthreads();
+    if (j + 2 < nch) {
+      load_a(0, k0 + 32 * KS * (j + 2));
+      load_b(b0, k0 + 32 * KS * (j + 2));
+    }
+    mma(b1, 1);
+  }
+
+  // 16x16 accumulator layout: lane (c = lane % 16, g = lane / 16), register i -> row 4g + i, col c
+  float *P = p.partial + (size_t)part * p.M * p.N;
+  const int n = n0 + r;
+#pragma unroll
+  for (int rb2 = 0; rb2 < 2; ++rb2)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * rb2 + 4 * q + i;
+      if (m < p.M && n < p.N) P[(size_t)m * p.N + n] = acc[rb2][i];
+    }
+}
+
 }  // namespace mtk
 
 using namespace mtk;
@@ -219,3 +319,10 @@ SKINNY(mtk_skinny_f16, DT_F16, skinny_gemm_resident)
 SKINNY(mtk_skinny_bf16, DT_BF16, skinny_gemm_resident)
 SKINNY(mtk_skinny_f16_long, DT_F16, skinny_gemm_long)
 SKINNY(mtk_skinny_bf16_long, DT_BF16, skinny_gemm_long)
+
+extern "C" __global__ void __launch_bounds__(256) mtk_skinny_parts_f16(const mtk_skinny_args a) {
+  skinny_gemm_parts<DT_F16>(a);
+}
+extern "C" __global__ void __launch_bounds__(256) mtk_skinny_parts_bf16(const mtk_skinny_args a) {
+  skinny_gemm_parts<DT_BF16>(a);
+}

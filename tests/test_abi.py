@@ -173,14 +173,28 @@ def test_gemm_kernel_select_dry():
 
 
 def test_gemm_small_m_large_k_plan():
-    # the reference's default run (matmul.swift:334): M = 32 fits a 128 tile, so the plan takes
-    # 128x128 tiles (24 of them) with the requested 30 partitions of 42 K-tiles, two-pass
+    # the reference's default run (matmul.swift:334): 16 < M <= 32 and long K go to the
+    # partial-writing skinny kernel (one workgroup per (partition, 64 columns): 30 x 48) with the
+    # requested 30 partitions of 42 K-tiles, then the two-pass reduce
     p = mtk.GemmPlan(None, 32, 3072, 80000, has_bias=True, split_k=30)
     d = p.describe()
+    assert "skinny partials M=32 N=3072 K=80000 split_k=30 k_tiles/split=42 grid=1440 " in d, d
+    assert d.endswith("kernels: mtk_skinny_parts_f16 mtk_splitk_reduce_f16")
+    assert p.workspace_bytes == 30 * 32 * 3072 * 4
+    # an explicit tile keeps the tile kernels (128x128: 24 tiles x 30 partitions)
+    d = mtk.GemmPlan(None, 32, 3072, 80000, has_bias=True, split_k=30, tile=128).describe()
     assert "tile=128x128 split_k=30 k_tiles/split=42 " in d and "grid=720 " in d
     assert d.endswith("kernels: mtk_gemm_f16_nt_128x128_d mtk_splitk_reduce_f16")
-    assert p.workspace_bytes == 30 * 32 * 3072 * 4
     assert "tile=256x256" in mtk.GemmPlan(None, 32, 3072, 80000, split_k=30, tile=256).describe()
+    # the in-workgroup schedule, split-K 1, short K, M <= 16 or transposed operands keep their kernels
+    assert "mtk_gemm_f16_nt_128x128_s" in mtk.GemmPlan(None, 32, 3072, 8192, split_k=4, split_mode="serial").describe()
+    assert "skinny" not in mtk.GemmPlan(None, 32, 3072, 80000, split_k=1).describe()
+    assert "skinny" not in mtk.GemmPlan(None, 32, 3072, 1024, split_k=4).describe()
+    assert "skinny partials" not in mtk.GemmPlan(None, 16, 3072, 80000, split_k=8).describe()
+    assert "skinny" not in mtk.GemmPlan(None, 32, 3072, 8192, split_k=4, trans_a=True).describe()
+    # the plan's own split: about four workgroups per CU over 48 column blocks
+    d = mtk.GemmPlan(None, 24, 3072, 16384, dtype="bf16", split_k=0).describe()
+    assert "skinny partials M=24" in d and "mtk_skinny_parts_bf16" in d, d
 
 
 @pytest.mark.parametrize("kw,status", [

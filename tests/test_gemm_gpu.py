@@ -288,10 +288,11 @@ def test_run_errors(dev):
     assert "workspace" in e.value.message
 
 
-@pytest.mark.parametrize("tile", [0, 256])
+@pytest.mark.parametrize("tile", [0, 128, 256])
 def test_reference_main_shape_large_k(dev, tile):
     # the reference's own default run (matmul.swift:334): M=32, N=3072, K=80000, split-K 30 (the
-    # plan's choice, 128x128 tiles, and 256x256 tiles); every output element is checked
+    # plan's choice, the partial-writing skinny kernel; 128x128 tiles; 256x256 tiles); every output
+    # element is checked
     M, N, K = 32, 3072, 80000
     A = oracle.normal(50, (M, K), 0, 1 / np.sqrt(K))
     B = oracle.normal(51, (N, K), 0, 1 / np.sqrt(K))
@@ -309,6 +310,22 @@ def test_config3_decode_skinny_full_size(dev):
     plan = mtk.GemmPlan(dev, M, N, K, dtype="bf16", has_bias=True, split_k=8)
     assert "skinny" in plan.describe() and "split_k=8" in plan.describe()
     check(dev, A, B, bias, dtype="bf16", split_k=8, label="config3")
+
+
+@pytest.mark.parametrize("M,N,K,split_k,dtype", [
+    (17, 1000, 4104, 5, "f16"), (32, 333, 2048, 2, "bf16"), (24, 4096, 16384, 0, "f16"), (32, 64, 2056, 3, "bf16"),
+    (29, 130, 70000, 30, "f16")])
+def test_skinny_partials_shapes(dev, M, N, K, split_k, dtype):
+    # 16 < M <= 32, long K: the partial-writing skinny kernel + the two-pass reduce (partitions
+    # of whole 64-element K-tiles; the last chunk of a partition and the last partition ragged;
+    # N not a multiple of the 64-column workgroup block)
+    plan = mtk.GemmPlan(dev, M, N, K, dtype=dtype, has_bias=True, split_k=split_k)
+    assert "skinny partials" in plan.describe(), plan.describe()
+    A = oracle.normal(60 + M, (M, K), 0, 1, dtype)
+    B = oracle.normal(70 + M, (N, K), 0, 1 / np.sqrt(K), dtype)
+    bias = oracle.normal(80 + M, (N,), 0, 0.05, dtype)
+    check(dev, A, B, bias, dtype=dtype, split_k=split_k, label="skinny partials")
+    check(dev, A, B, None, dtype=dtype, split_k=split_k, label="skinny partials, no bias")
 
 
 @pytest.mark.parametrize("M,N,K,split_k,dtype", [
