@@ -210,60 +210,74 @@ __device__ __forceinline__ void skinny_gemm_long(const mtk_skinny_args &p) {
 
 // Partial-writing kernel for 16 < M <= 32 and long K, the shape of the reference's default run
 // (f16 32 x 3072 x 80000, split-K 30; matmul.swift main()): one workgroup per (K partition,
-// 64 columns), four wavefronts of 16 columns. It writes the two-pass schedule's fp32 partials
-// [split_k][M][N] (uniform partitions of k_per_split elements); the reduce kernel then adds them in
-// partition order and the bias. Per 512-element chunk of the partition:
-//   * A's 32 rows are staged once for the workgroup (direct-to-LDS, double buffered; lane l of
-//     row m loads chunk l ^ (m & 15), the slot it lands in is l), each wavefront loading 8 rows;
-//   * B's 16 rows of each wavefront are read 1 KB of one row per instruction (whole cache lines,
-//     non-temporal, double buffered in registers) and transposed through the wavefront's own LDS
-//     region as in the decode kernel;
-//   * 16 K steps of two 16x16x32 MFMAs (rows 0-15 and 16-31 of A) on one B fragment each.
+// 64 columns), four wavefronts of 16 columns, two workgroups per CU. It writes the two-pass
+// schedule's fp32 partials [split_k][M][N] (uniform partitions of k_per_split elements); the
+// reduce kernel then adds them in partition order and the bias. Per 256-element chunk of the
+// partition, loads two chunks ahead (three register buffers):
+//   * every load instruction reads 512 bytes of each of two rows (whole cache lines): each
+//     wavefront loads 8 of A's 32 rows and its own 16 B rows;
+//   * the wavefronts write their A rows into the chunk's shared LDS buffer (three buffers; row m,
+//     16-byte chunk c at slot c ^ (m & 15)), then a barrier; B goes through the wavefront's own
+//     LDS region, transposed as in the decode kernel;
+//   * 8 K steps of two 16x16x32 MFMAs (rows 0-15 and 16-31 of A) on one B fragment each.
+// A is staged through registers rather than direct-to-LDS loads: with those in flight the
+// compiler makes every LDS read wait for them (vmcnt(0)), which serializes the chunks.
 // Rows m >= M, columns n >= N and K past the partition read zero.
 template <int DT>
 __device__ __forceinline__ void skinny_gemm_parts(const mtk_skinny_args &p) {
-  constexpr int KS = kSkinnyResident;  // 16 K steps of 32: 512 elements per chunk
-  constexpr int kStreamPolicy = 2;     // non-temporal B loads
-  __shared__ __attribute__((aligned(1024))) u32x4 abuf[2][32][64];  // A chunk: 32 rows x 1 KB
-  __shared__ __attribute__((aligned(16))) u32x4 tr[4][KS][64];      // per wavefront: 16 rows x 1 KB
+  constexpr int KS = 8;              // MFMA K steps (of 32) per chunk: 256 elements, 512 bytes a row
+  constexpr int kStreamPolicy = 2;   // non-temporal B loads
+  __shared__ __attribute__((aligned(1024))) u32x4 abuf[3][32][32];  // A chunks: 32 rows x 512 B
+  __shared__ __attribute__((aligned(16))) u32x4 tr[4][16][32];      // per wavefront: 16 rows x 512 B
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int ncb = (p.N + 63) / 64;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);  // consecutive ids (the column blocks of one
-  const int part = id / ncb, cb = id - part * ncb;   // partition) share an XCD and its A
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int part = id / ncb, cb = id - part * ncb;
   const int k0 = part * p.k_per_split;
   const int k1 = min(p.K, k0 + p.k_per_split);
   const int nch = k1 > k0 ? (k1 - k0 + 32 * KS - 1) / (32 * KS) : 0;
-  const int n0 = cb * 64 + 16 * w;  // this wavefront's first column
+  const int n0 = cb * 64 + 16 * w;
   const rsrc_t ra = make_rsrc(p.A, p.a_bytes);
   const rsrc_t rb = make_rsrc(p.B, p.b_bytes);
   const int r = lane & 15, q = lane >> 4;
-  u32x4(&t)[KS][64] = tr[w];
+  const int hl = lane >> 5, sl = lane & 31;  // load instruction lanes: row 2i + hl, 16-byte chunk sl
+  u32x4(&t)[16][32] = tr[w];
 
-  auto load_a = [&](int buf, int kc) {
+  // A rows 8w + 2i + hl and B rows n0 + 2i + hl: chunk sl (16 bytes) of the chunk's 512 bytes
+  auto load_a = [&](u32x4 (&ar)[4], int kc) {
+    const int k = kc + 8 * sl;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int m = 8 * w + i;
-      const int k = kc + 8 * (lane ^ (m & 15));
-      lds_direct16(ra, (char *)&abuf[buf][m][0],
-                   (m < p.M && k < k1) ? (uint32_t)m * (uint32_t)p.lda * 2u + (uint32_t)k * 2u : kOOB);
+    for (int i = 0; i < 4; ++i) {
+      const int m = 8 * w + 2 * i + hl;
+      ar[i] = buf_load16(ra, (m < p.M && k < k1) ? (uint32_t)m * (uint32_t)p.lda * 2u + (uint32_t)k * 2u : kOOB);
     }
   };
-  auto load_b = [&](u32x4 (&b)[KS], int kc) {
-    const int k = kc + 8 * lane;
+  auto load_b = [&](u32x4 (&b)[8], int kc) {
+    const int k = kc + 8 * sl;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int n = n0 + s;
-      b[s] = __builtin_amdgcn_raw_buffer_load_b128(
+    for (int i = 0; i < 8; ++i) {
+      const int n = n0 + 2 * i + hl;
+      b[i] = __builtin_amdgcn_raw_buffer_load_b128(
           rb, (n < p.N && k < k1) ? (uint32_t)n * (uint32_t)p.ldb * 2u + (uint32_t)k * 2u : kOOB, 0, kStreamPolicy);
     }
   };
-  f32x4 acc[2] = {f32x4{}, f32x4{}};
-  // chunk j: B fragments through this wavefront's LDS region, A fragments from the shared chunk
-  auto mma = [&](const u32x4 (&b)[KS], int buf) {
+  // row m, chunk c -> slot c ^ (m & 15)
+  auto store_a = [&](const u32x4 (&ar)[4], int buf) {
 #pragma unroll
-    for (int s = 0; s < KS; ++s) t[s][lane ^ s] = b[s];
+    for (int i = 0; i < 4; ++i) {
+      const int m = 8 * w + 2 * i + hl;
+      abuf[buf][m][sl ^ (m & 15)] = ar[i];
+    }
+  };
+  f32x4 acc[2] = {f32x4{}, f32x4{}};
+  auto mma = [&](const u32x4 (&b)[8], int buf) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = 2 * i + hl;
+      t[row][sl ^ (row & 15)] = b[i];
+    }
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const u32x4 bf = t[r][(4 * s + q) ^ r];
@@ -272,29 +286,31 @@ __device__ __forceinline__ void skinny_gemm_parts(const mtk_skinny_args &p) {
     }
   };
 
-  u32x4 b0[KS], b1[KS];
-  if (nch > 0) {
-    load_a(0, k0);
-    load_b(b0, k0);
-  }
-  for (int j = 0; j < nch; j += 2) {
-    // chunk j (A in buffer 0, B in b0) has landed; every wavefront is done with buffer 1
-    wait_vmem();
-    __syncthreads();
-    if (j + 1 < nch) {
-      load_a(1, k0 + 32 * KS * (j + 1));
-      load_b(b1, k0 + 32 * KS * (j + 1));
-    }
-    mma(b0, 0);
+  u32x4 a0[4], a1[4], a2[4], b0[8], b1[8], b2[8];
+  // Chunk j: A (its wavefront's 8 rows) into LDS buffer j % 3, a raw barrier (LDS writes done:
+  // lgkmcnt(0); __syncthreads' fence would also wait for the loads of chunks j + 1 and j + 2),
+  // the loads of chunk j + 2, then the chunk's MFMAs. Loads are issued unconditionally (chunks
+  // past the partition read zeros), so the compiler's waits for each register buffer are exact.
+  auto step = [&](int j, const u32x4 (&ac)[4], const u32x4 (&bc)[8], int buf, u32x4 (&an)[4], u32x4 (&bn)[8]) {
+    store_a(ac, buf);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    load_a(an, k0 + 32 * KS * (j + 2));
+    load_b(bn, k0 + 32 * KS * (j + 2));
+    mma(bc, buf);
+  };
+  load_a(a0, k0);
+  load_b(b0, k0);
+  load_a(a1, k0 + 32 * KS);
+  load_b(b1, k0 + 32 * KS);
+  for (int j = 0; j < nch; j += 3) {
+    step(j, a0, b0, 0, a2, b2);
     if (j + 1 >= nch) break;
-    wait_vmem();
-    __syncthreads();
-    if (j + 2 < nch) {
-      load_a(0, k0 + 32 * KS * (j + 2));
-      load_b(b0, k0 + 32 * KS * (j + 2));
-    }
-    mma(b1, 1);
+    step(j + 1, a1, b1, 1, a0, b0);
+    if (j + 2 >= nch) break;
+    step(j + 2, a2, b2, 2, a1, b1);
   }
+  wait_vmem();  // the chunks issued past the partition (zeros) land before the workgroup ends
 
   // 16x16 accumulator layout: lane (c = lane % 16, g = lane / 16), register i -> row 4g + i, col c
   float *P = p.partial + (size_t)part * p.M * p.N;
