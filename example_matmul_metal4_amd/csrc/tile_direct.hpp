@@ -22,9 +22,10 @@
 // Chunk swizzle there: chunk ^ 4*(row%4), which spreads the 8 rows one read touches over 16
 // distinct 16-byte bank groups.
 //
-// Pipeline: two LDS stages, one barrier per 64-deep K-tile; each k-step's MFMAs are interleaved in
-// groups with one 1 KB load of the next tile and the next k-step's fragment reads
-// (scheduling fences keep the compiler from regrouping them).
+// Pipeline: two LDS stages, one barrier per 64-deep K-tile, in its middle; fragments are read two
+// k-steps ahead into a ring of four k-step buffers, and the loads of K-tile kt + 2 go into the
+// stage of K-tile kt during its last two k-steps. Each k-step's MFMAs are interleaved in groups with
+// those loads and the fragment reads (scheduling fences keep the compiler from regrouping them).
 #pragma once
 
 #include "tile_gemm.hpp"
@@ -33,9 +34,6 @@
 #define MTK_SLOT_RING 2
 #endif
 
-#ifndef MTK_LOAD_GROUPS
-#define MTK_LOAD_GROUPS 8
-#endif
 
 namespace mtk {
 
@@ -50,7 +48,7 @@ struct OpRows {
   static constexpr bool kIsConv = false;
   static constexpr int kLoads = ROWS / (8 * NW);  // 1 KB blocks per wave per K-tile
   static constexpr bool kNeedsTail = true;  // the last K-tile's fragments are masked at K
-  static constexpr bool kAsmFrag = false;
+  static constexpr int kReadsPerFrag = 1;
   uint32_t off[kLoads];
   int blk0;
   int ld;
@@ -84,7 +82,7 @@ struct OpRows {
   // K offset of the fragment a lane reads for k-step ks of K-tile kt
   __device__ static __forceinline__ int frag_k0(int kt, int ks, int lane) { return kt * kBK + 16 * ks + 8 * (lane >> 5); }
   __device__ __forceinline__ u32x4 frag(const char *lds, int rowblk, int ks, int lane) const {
-    return *(const u32x4 *)(lds + lds_off(rowblk + (lane & 31), 2 * ks + (lane >> 5)));
+    return ds_read_b128_at<0>(lds_addr(lds) + lds_off(rowblk + (lane & 31), 2 * ks + (lane >> 5)));
   }
 };
 
@@ -98,7 +96,7 @@ struct OpConv {
   static constexpr bool kIsConv = true;
   static constexpr int kLoads = ROWS / (8 * NW);
   static constexpr bool kNeedsTail = false;  // K = taps * C is a multiple of 64
-  static constexpr bool kAsmFrag = false;
+  static constexpr int kReadsPerFrag = 1;
   int pb8[kLoads];
   uint32_t pm[kLoads];
   int blk0;
@@ -149,6 +147,7 @@ struct OpConv {
     lds_direct16(r, lds + (blk0 + q) * 1024, ok ? (uint32_t)(pb8[q] + tp.elems) * 2u : kOOB);
   }
   __device__ __forceinline__ u32x4 frag(const char *lds, int rowblk, int ks, int lane) const {
+    // a plain LDS read: the convolution pipeline waits for every read before each k-step
     return *(const u32x4 *)(lds + lds_off(rowblk + (lane & 31), 2 * ks + (lane >> 5)));
   }
 };
@@ -162,11 +161,7 @@ struct OpColsT {
   static constexpr int kRowBytes = COLS * 2;
   static constexpr int kLoads = COLS / (8 * NW);  // 64 rows x kRowBytes / 1 KB / NW waves
   static constexpr bool kNeedsTail = false;  // rows k >= K are past the operand: read as zero
-  // Fragment reads are inline asm: the compiler's wait insertion cannot tell the transposed read
-  // builtin apart from the in-flight direct-to-LDS writes of the other stage and would wait for
-  // all of them (vmcnt(0)) before every read. The kernel waits for these reads itself
-  // (frag_wait) before the MFMAs that consume them.
-  static constexpr bool kAsmFrag = true;
+  static constexpr int kReadsPerFrag = 2;  // two transposed 8-byte reads
   uint32_t off[kLoads];
   int blk0;
   uint32_t kstride;  // bytes per K-tile (64 rows)
@@ -203,6 +198,35 @@ struct OpColsT {
   }
 };
 
+// ---------------------------------------------------------------- waits
+
+// vmcnt(N): at most N vector-memory operations of this wave outstanding (direct-to-LDS loads
+// included); LDS reads are not waited for.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// Fragments filled by inline-asm LDS reads are handed to their consumers through empty asm
+// statements that take them as in/out operands: no use can be scheduled above the wait before it.
+template <int TA, int TB>
+__device__ __forceinline__ void frag_tie(u32x4 (&fa)[TA], u32x4 (&fb)[TB]) {
+#pragma unroll
+  for (int i = 0; i < TA; ++i) asm volatile("" : "+v"(fa[i]));
+#pragma unroll
+  for (int j = 0; j < TB; ++j) asm volatile("" : "+v"(fb[j]));
+}
+
+// lgkmcnt(N): at most N LDS reads of this wave outstanding (they complete in issue order), then
+// the fragments of the k-step about to run are tied to the wait.
+template <int N, int TA, int TB>
+__device__ __forceinline__ void frag_wait(u32x4 (&fa)[TA], u32x4 (&fb)[TB]) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
+  frag_tie(fa, fb);
+}
+
 // ---------------------------------------------------------------- the kernel body
 
 // SERIAL (GEMM split-K on a tile grid that already fills the chip, at most 4 partitions): one
@@ -222,11 +246,9 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   static_assert(TM >= TN, "fragment reads are paired per row block");
   constexpr int kStage = (BM + BN) * 128;
   constexpr int PA = AOP::kLoads, PB = BOP::kLoads;
-  // The next K-tile's loads go out in the first kLoadGroups MFMA groups of the current one, so
-  // they have most of the tile's MFMA time to land before the end-of-tile wait.
-  constexpr int kGroups = (kBK / 16) * TM;
-  // every load of the next K-tile is issued before the last k-step, where the barrier waits for it
-  constexpr int kLoadGroups = MTK_LOAD_GROUPS < kGroups - TM ? MTK_LOAD_GROUPS : kGroups - TM;
+  // The loads of K-tile kt + 2 go out in the MFMA groups of k-steps 2 and 3 of K-tile kt; the
+  // barrier in the middle of K-tile kt + 1 waits for them.
+  constexpr int kLoadGroups = 2 * TM;
   constexpr int kPerGroup = (PA + PB + kLoadGroups - 1) / kLoadGroups;
   constexpr int kReadsPerGroup = (TM + TN + TM - 1) / TM;  // next k-step's fragment reads per MFMA group
 
@@ -302,198 +324,268 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   };
   int split_end = SERIAL ? split_first_tile(a, 1, t) : 0;  // SERIAL: first K-tile of the next partition
   int parked = 0;                                           // SERIAL: partitions parked in the workspace
-  // SERIAL: the K-tile after a partition boundary had its next tile's loads issued at the boundary,
-  // ahead of the slot stores; it waits for those loads only (vmcnt(kSlotStores): vector memory
-  // operations complete in issue order, so at most the stores are then outstanding).
-  bool preissued = false;
   constexpr int kSlotStores = TM * TN * 4;  // slot store instructions per wavefront and boundary
-  static_assert(kSlotStores < 64, "vmcnt range");
-  if (kt0 < kt1) issue_all(smem, kt0);
-  wait_vmem();
-  __syncthreads();
+  static_assert(!SERIAL || kSlotStores < 64, "vmcnt range");
 
-  // Fragments of the first k-step of the first tile. Afterwards the last k-step of every tile
-  // reads the next tile's first fragments: the barrier sits before that k-step (its own fragments
-  // are already in registers), so its MFMAs cover the latency of those reads.
-  u32x4 fa[2][TM], fb[2][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) fa[0][i] = opa.frag(smem, wave_m * WTM + i * 32, 0, lane);
-#pragma unroll
-  for (int j = 0; j < TN; ++j) fb[0][j] = opb.frag(smem + BM * 128, wave_n * WTN + j * 32, 0, lane);
+  if constexpr (!AOP::kIsConv) {
+    // Fragments: a ring of four k-step buffers (slot s holds k-step s of a K-tile), read two k-steps
+    // ahead. The reads are inline asm, which the compiler does not track: it would otherwise make
+    // every LDS read wait for the direct-to-LDS loads in flight, and at the loop's back edge for
+    // every read. Each k-step waits for its own reads only (lgkmcnt counts them in issue order).
+    constexpr int kStepReads = TM * AOP::kReadsPerFrag + TN * BOP::kReadsPerFrag;
+    static_assert(kStepReads <= 15, "lgkmcnt range");
+    u32x4 fa[4][TM], fb[4][TN];
+    auto read_step = [&](auto s_c, const char *st) {
+      constexpr int S = decltype(s_c)::value;
+  #pragma unroll
+      for (int i = 0; i < TM; ++i) fa[S][i] = opa.frag(st, wave_m * WTM + i * 32, S, lane);
+  #pragma unroll
+      for (int j = 0; j < TN; ++j) fb[S][j] = opb.frag(st + BM * 128, wave_n * WTN + j * 32, S, lane);
+    };
 
-  // SERIAL: the K loop runs once per partition (the pipeline carries on across the boundary: the
-  // last K-tile of a partition prefetches the next one's first); the partition sum is parked
-  // between the runs.
-  // One K-tile of the pipeline. PRE (SERIAL only): the first K-tile after a partition boundary,
-  // whose next tile's loads went out at the boundary.
-  auto ktile = [&](const int kt, auto pre_c) {
+    // Prologue: K-tiles kt0 and kt0 + 1 into the two stages, the first two k-steps' fragments.
+    if (kt0 < kt1) {
+      issue_all(smem, kt0);
+      issue_all(smem + kStage, min(kt0 + 1, kt1 - 1));
+      vm_wait<PA + PB>();  // the first K-tile's loads (the second's may still be in flight)
+      __builtin_amdgcn_s_barrier();
+      read_step(std::integral_constant<int, 0>{}, smem);
+      read_step(std::integral_constant<int, 1>{}, smem);
+    }
+    // Asm reads land in their registers asynchronously, unseen by the compiler: wherever code it
+    // schedules freely follows (here, the loop entry; the partition boundary; the end), the reads in
+    // flight are waited for first, so a register copy or spill never takes a value before it lands.
+    frag_wait<0>(fa[0], fb[0]);
+    frag_tie(fa[1], fb[1]);
+
+    // One K-tile: four k-steps of TM groups of TN MFMAs. K-steps 0 and 1 read k-steps 2 and 3 of this
+    // K-tile's stage; the barrier before k-step 2 (every wave done reading the stage, K-tile kt + 1
+    // landed) frees the stage, so k-steps 2 and 3 read k-steps 0 and 1 of the next K-tile and load
+    // K-tile kt + 2 into this stage, which the barrier of the next K-tile waits for. Past the end the
+    // last K-tile is reloaded (L2 hits, never computed) instead of a branch. PRE (SERIAL only): the
+    // first K-tile after a partition boundary, whose wait leaves the boundary's slot stores in flight
+    // (vector memory operations complete in issue order; the next K-tile's loads went out before
+    // them).
+    auto ktile = [&](const int kt, auto pre_c) {
       constexpr bool PRE = decltype(pre_c)::value;
       const int cur = (kt - kt0) & 1;
+      char *sc = smem + cur * kStage;
+      const char *sn = smem + (cur ^ 1) * kStage;
+      const int kn = min(kt + 2, kt1 - 1);
+      typename std::conditional<AOP::kIsConv, typename OpConv<BM, NW>::Tap, int>::type tp{};
+      if constexpr (AOP::kIsConv) tp = opa.tap(a, kn);
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<0, kBK / 16>([&](auto k_c) {
+        constexpr int ks = decltype(k_c)::value;
+        constexpr int kr = (ks + 2) & 3;  // the k-step read during this one (ring slot)
+        if constexpr (ks == 2) {
+          frag_wait<0>(fa[2], fb[2]);
+          frag_tie(fa[3], fb[3]);
+          if constexpr (PRE)
+            vm_wait<kSlotStores>();
+          else
+            vm_wait<0>();
+          __builtin_amdgcn_s_barrier();
+        } else {
+          frag_wait<kStepReads>(fa[ks], fb[ks]);
+        }
+        const char *src = ks < 2 ? sc : sn;
+  #pragma unroll
+        for (int i = 0; i < TM; ++i) {
+  #pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa[ks][i], fb[ks][j], acc[i][j]);
+          if constexpr (ks >= 2) {
+  #pragma unroll
+            for (int u = 0; u < kPerGroup; ++u) {
+              const int q = ((ks - 2) * TM + i) * kPerGroup + u;
+              if (q < PA) {
+                if constexpr (AOP::kIsConv)
+                  opa.issue(ra, sc, q, tp);
+                else
+                  opa.issue(ra, sc, q, kn);
+              } else if (q < PA + PB) {
+                opb.issue(rb, sc + BM * 128, q - PA, kn);
+              }
+            }
+          }
+          // The next k-step's first MFMA group needs every B fragment and only A fragment 0, later
+          // groups one more A fragment each: read the B fragments in the first groups, then A.
+  #pragma unroll
+          for (int u = 0; u < kReadsPerGroup; ++u) {
+            const int slot = i * kReadsPerGroup + u;
+            if (slot < TN)
+              fb[kr][slot] = opb.frag(src + BM * 128, wave_n * WTN + slot * 32, kr, lane);
+            else if (slot < TN + TM)
+              fa[kr][slot - TN] = opa.frag(src, wave_m * WTM + (slot - TN) * 32, kr, lane);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      });
+    };
+
+    // SERIAL: the K loop runs once per partition (the pipeline carries on across the boundary); the
+    // partition sum is parked between the runs.
+    int kt = kt0;
+    bool pre = false;
+    for (;;) {
+      const int kstop = SERIAL ? min(split_end, kfull) : kfull;
+      if constexpr (SERIAL) {
+        if (pre && kt < kstop) ktile(kt++, std::true_type{});
+        pre = false;
+      }
+      for (; kt < kstop; ++kt) ktile(kt, std::false_type{});
+      if constexpr (!SERIAL) {
+        break;
+      } else {
+        // Partition boundaries lie strictly inside K (at most split_k-1 of them); the K loop ends
+        // anywhere else (or at K itself) after the last partition. Only boundaries park, so every
+        // slot written is one of this tile's split_k-1.
+        if (kt != split_end || split_end >= a.k_tiles || parked >= a.split_k - 1) break;
+        pre = true;
+        frag_wait<0>(fa[0], fb[0]);
+        frag_tie(fa[1], fb[1]);
+        if (parked == 0) {
+  #pragma unroll
+          for (int i = 0; i < TM; ++i)
+  #pragma unroll
+            for (int j = 0; j < TN; ++j)
+  #pragma unroll
+              for (int q = 0; q < 4; ++q)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(u32x4, f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                                    acc[i][j][4 * q + 3]}),
+                    rslot, slot_at(i, j, q), 0, kStorePolicy);
+        } else {
+          // slot += partition sum, one accumulator block at a time, the next kSlotRing-1 blocks'
+          // loads in flight
+          f32x4 ring[kSlotRing][4];
+  #pragma unroll
+          for (int b = 0; b + 1 < kSlotRing; ++b)
+  #pragma unroll
+            for (int q = 0; q < 4; ++q) ring[b][q] = slot_load(b % TM, b / TM, q);
+  #pragma unroll
+          for (int b = 0; b < TM * TN; ++b) {
+            const int i = b % TM, j = b / TM;
+            constexpr int kAhead = kSlotRing - 1;
+            if (b + kAhead < TM * TN) {
+  #pragma unroll
+              for (int q = 0; q < 4; ++q) ring[(b + kAhead) % kSlotRing][q] = slot_load((b + kAhead) % TM, (b + kAhead) / TM, q);
+            }
+  #pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const f32x4 v = ring[b % kSlotRing][q] +
+                              f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rslot, slot_at(i, j, q), 0,
+                                                     kStorePolicy);
+            }
+          }
+        }
+        ++parked;
+        split_end = split_first_tile(a, parked + 1, t);
+  #pragma unroll
+        for (int i = 0; i < TM; ++i)
+  #pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
+      }
+    }
+    // The reads of the last K-tile's k-steps 2 and 3 (fragments of the partial last K-tile, or of a
+    // K-tile that is never computed) may still be in flight.
+    frag_wait<0>(fa[0], fb[0]);
+    frag_tie(fa[1], fb[1]);
+    if constexpr (kAnyTail) {
+      if (tail_here) {
+        // The partial last K-tile, already in LDS (loaded as a next K-tile by the loop, or by the
+        // prologue when it is the only one) with its first two k-steps' fragments in slots 0 and 1:
+        // the same k-steps, fragments masked at K.
+        const char *st = smem + ((kfull - kt0) & 1) * kStage;
+        static_for<0, kBK / 16>([&](auto k_c) {
+          constexpr int ks = decltype(k_c)::value;
+          frag_wait<(ks < 2 ? kStepReads : 0)>(fa[ks], fb[ks]);
+          if constexpr (AOP::kNeedsTail) {
+  #pragma unroll
+            for (int i = 0; i < TM; ++i) fa[ks][i] = AOP::mask(fa[ks][i], AOP::frag_k0(kfull, ks, lane), a.K);
+          }
+          if constexpr (BOP::kNeedsTail) {
+  #pragma unroll
+            for (int j = 0; j < TN; ++j) fb[ks][j] = BOP::mask(fb[ks][j], BOP::frag_k0(kfull, ks, lane), a.K);
+          }
+  #pragma unroll
+          for (int i = 0; i < TM; ++i) {
+  #pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa[ks][i], fb[ks][j], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          if constexpr (ks < 2) read_step(std::integral_constant<int, ks + 2>{}, st);
+        });
+      }
+    }
+  } else {
+    // Convolution: fragments one k-step ahead (two buffers); the loads of K-tile kt + 1 go out in
+    // the first MFMA groups of K-tile kt and are waited for at one barrier before its last k-step.
+    // (The two-ahead ring measured 2-5 % slower on the gather: its loads of K-tile kt + 2 come in
+    // the second half of K-tile kt.)
+    static_assert(!SERIAL && !kAnyTail, "convolutions never split K and have whole K-tiles");
+    constexpr int kGroups1 = (kBK / 16) * TM;
+    constexpr int kLoadGroups1 = 8 < kGroups1 - TM ? 8 : kGroups1 - TM;
+    constexpr int kPerGroup1 = (PA + PB + kLoadGroups1 - 1) / kLoadGroups1;
+    if (kt0 < kt1) issue_all(smem, kt0);
+    wait_vmem();
+    __syncthreads();
+    u32x4 ga[2][TM], gb[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) ga[0][i] = opa.frag(smem, wave_m * WTM + i * 32, 0, lane);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) gb[0][j] = opb.frag(smem + BM * 128, wave_n * WTN + j * 32, 0, lane);
+    for (int kt = kt0; kt < kt1; ++kt) {
+      const int cur = (kt - kt0) & 1;
       char *nxt = smem + (cur ^ 1) * kStage;
-      // The next tile is the partial last K-tile when there is one. Without one, the last iteration
-      // reloads the current tile into the idle stage (L2 hits, never computed) instead of reaching
-      // into another split's K range: branch-free.
+      // the last iteration reloads the current K-tile into the idle stage (L2 hits, never computed)
       const int kn = min(kt + 1, kt1 - 1);
       const char *sa = smem + cur * kStage;
       const char *sb = sa + BM * 128;
-      typename std::conditional<AOP::kIsConv, typename OpConv<BM, NW>::Tap, int>::type tp{};
-      if constexpr (AOP::kIsConv) tp = opa.tap(a, kn);
+      const auto tp = opa.tap(a, kn);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int ks = 0; ks < kBK / 16; ++ks) {
         const int c = ks & 1, nx = c ^ 1;
         constexpr int kLast = kBK / 16 - 1;
         if (ks == kLast) {
-          // the next tile has landed (own loads: vmcnt; everyone's: barrier) and every wave is done
-          // reading this tile's stage, which the next iteration starts to overwrite
-          if constexpr (PRE) {
-            // the slot stores issued after this tile's loads may still be in flight (raw barrier:
-            // __syncthreads' fence would wait for them)
-            __builtin_amdgcn_s_waitcnt((kSlotStores & 15) | ((kSlotStores >> 4) << 14) | 0x70);  // vmcnt(S) lgkmcnt(0)
-            __builtin_amdgcn_s_barrier();
-          } else {
-            wait_vmem();
-            __syncthreads();
-          }
+          // the next K-tile has landed and every wave is done reading this K-tile's stage
+          wait_vmem();
+          __syncthreads();
         }
-        // this k-step's fragments read by inline asm (one k-step earlier)
-        if constexpr (AOP::kAsmFrag) lgkm_wait0(fa[c]);
-        if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[c]);
+        // this k-step's B fragments, read by inline asm one k-step earlier (the plain A reads are
+        // waited for by the compiler)
+        lgkm_wait0(gb[c]);
         const char *ra_ = ks < kLast ? sa : nxt;
         const char *rb_ = ks < kLast ? sb : nxt + BM * 128;
         const int ksn = ks < kLast ? ks + 1 : 0;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
 #pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa[c][i], fb[c][j], acc[i][j]);
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(ga[c][i], gb[c][j], acc[i][j]);
 #pragma unroll
-          for (int u = 0; u < kPerGroup; ++u) {
-            const int q = (ks * TM + i) * kPerGroup + u;
-            if (PRE) {
-              // issued at the partition boundary
-            } else if (q < PA) {
-              if constexpr (AOP::kIsConv)
-                opa.issue(ra, nxt, q, tp);
-              else
-                opa.issue(ra, nxt, q, kn);
-            } else if (q < PA + PB) {
+          for (int u = 0; u < kPerGroup1; ++u) {
+            const int q = (ks * TM + i) * kPerGroup1 + u;
+            if (q < PA)
+              opa.issue(ra, nxt, q, tp);
+            else if (q < PA + PB)
               opb.issue(rb, nxt + BM * 128, q - PA, kn);
-            }
           }
-          // The next k-step's first MFMA group needs every B fragment and only A fragment 0, later
-          // groups one more A fragment each: read the B fragments in the first groups, then A.
 #pragma unroll
           for (int u = 0; u < kReadsPerGroup; ++u) {
             const int slot = i * kReadsPerGroup + u;
             if (slot < TN)
-              fb[nx][slot] = opb.frag(rb_, wave_n * WTN + slot * 32, ksn, lane);
+              gb[nx][slot] = opb.frag(rb_, wave_n * WTN + slot * 32, ksn, lane);
             else if (slot < TN + TM)
-              fa[nx][slot - TN] = opa.frag(ra_, wave_m * WTM + (slot - TN) * 32, ksn, lane);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-  };
-
-  int kt = kt0;
-  for (;;) {
-    const int kstop = SERIAL ? min(split_end, kfull) : kfull;
-    if constexpr (SERIAL) {
-      if (preissued && kt < kstop) ktile(kt++, std::true_type{});
-      preissued = false;
-    }
-    for (; kt < kstop; ++kt) ktile(kt, std::false_type{});
-    if constexpr (!SERIAL) {
-      break;
-    } else {
-      // Partition boundaries lie strictly inside K (at most split_k-1 of them); the K loop ends
-      // anywhere else (or at K itself) after the last partition. Only boundaries park, so every
-      // slot written is one of this tile's split_k-1.
-      if (kt != split_end || split_end >= a.k_tiles || parked >= a.split_k - 1) break;
-      // The loads K-tile kt would issue (tile kt + 1, into the stage of tile kt - 1, which every
-      // wave finished reading before the last barrier) go out now, ahead of the slot traffic.
-      issue_all(smem + ((((kt - kt0) & 1)) ^ 1) * kStage, min(kt + 1, kt1 - 1));
-      preissued = true;
-      if (parked == 0) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              __builtin_amdgcn_raw_buffer_store_b128(
-                  __builtin_bit_cast(u32x4, f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                                                  acc[i][j][4 * q + 3]}),
-                  rslot, slot_at(i, j, q), 0, kStorePolicy);
-      } else {
-        // slot += partition sum, one accumulator block at a time, the next kSlotRing-1 blocks'
-        // loads in flight
-        f32x4 ring[kSlotRing][4];
-#pragma unroll
-        for (int b = 0; b + 1 < kSlotRing; ++b)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) ring[b][q] = slot_load(b % TM, b / TM, q);
-#pragma unroll
-        for (int b = 0; b < TM * TN; ++b) {
-          const int i = b % TM, j = b / TM;
-          constexpr int kAhead = kSlotRing - 1;
-          if (b + kAhead < TM * TN) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) ring[(b + kAhead) % kSlotRing][q] = slot_load((b + kAhead) % TM, (b + kAhead) / TM, q);
-          }
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f32x4 v = ring[b % kSlotRing][q] +
-                            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rslot, slot_at(i, j, q), 0,
-                                                   kStorePolicy);
-          }
-        }
-      }
-      ++parked;
-      split_end = split_first_tile(a, parked + 1, t);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
-    }
-  }
-  // The last prefetch (of a tile that is never computed) may still be in flight. Inline-asm reads
-  // land in their registers asynchronously, so they must be waited for while the registers are
-  // still theirs: the wait carries them as operands.
-  if constexpr (AOP::kAsmFrag) lgkm_wait0(fa[0]);
-  if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[0]);
-  if constexpr (kAnyTail) {
-    if (tail_here) {
-      // The partial last K-tile, already in LDS (loaded as the last loop iteration's next tile,
-      // or by the prologue when it is the only tile): same k-steps, fragments masked at K.
-      const char *sa = smem + ((kfull - kt0) & 1) * kStage;
-      const char *sb = sa + BM * 128;
-#pragma unroll
-      for (int ks = 0; ks < kBK / 16; ++ks) {
-        const int c = ks & 1, nx = c ^ 1;
-        if constexpr (AOP::kAsmFrag) lgkm_wait0(fa[c]);
-        if constexpr (BOP::kAsmFrag) lgkm_wait0(fb[c]);
-        if constexpr (AOP::kNeedsTail) {
-#pragma unroll
-          for (int i = 0; i < TM; ++i) fa[c][i] = AOP::mask(fa[c][i], AOP::frag_k0(kfull, ks, lane), a.K);
-        }
-        if constexpr (BOP::kNeedsTail) {
-#pragma unroll
-          for (int j = 0; j < TN; ++j) fb[c][j] = BOP::mask(fb[c][j], BOP::frag_k0(kfull, ks, lane), a.K);
-        }
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-#pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(fa[c][i], fb[c][j], acc[i][j]);
-          if (ks + 1 < kBK / 16) {
-            fa[nx][i] = opa.frag(sa, wave_m * WTM + i * 32, ks + 1, lane);
-            if (i < TN) fb[nx][i] = opb.frag(sb, wave_n * WTN + i * 32, ks + 1, lane);
+              ga[nx][slot - TN] = opa.frag(ra_, wave_m * WTM + (slot - TN) * 32, ksn, lane);
           }
           __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
+    // the last prefetch (of a K-tile never computed) may still be in flight
+    lgkm_wait0(gb[0]);
   }
 
   // ---- epilogue. 32x32 accumulator layout: lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4,
