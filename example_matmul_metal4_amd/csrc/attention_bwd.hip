@@ -19,6 +19,8 @@
 //                  queries: P and dS leave the
 //                  accumulators as the B operands of dV^T += dO^T.P and dK^T += Q^T.dS, whose
 //                  A operands are transposed LDS reads (ds_read_b64_tr_b16) of the dO / Q tiles.
+//                  Software-pipelined: the S / dP MFMAs of tile i + 1 run interleaved with the
+//                  softmax work of tile i (one element per MFMA), then the dV / dK MFMAs of tile i.
 //   attn_bwd_dq    one workgroup per 256 queries, 8 wavefronts x 32 queries (the forward's shape):
 //                  S^T = K.Q^T and dP^T = V.dO^T with the query as the accumulator column, then
 //                  dQ^T += K^T.dS^T with K^T read transposed from LDS.
@@ -128,10 +130,13 @@ __device__ __forceinline__ void attn_bwd_pre(const mtk_attn_bwd_kargs &a) {
 
 template <int DT, bool CAUSAL>
 __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
-  // per stage: Q rows, Q transposed-read copy, dO rows, dO transposed-read copy, then the tile's
-  // 64 lse and 64 D values (1 KB slots, filled by one direct-to-LDS instruction each)
-  constexpr int kStageBytes = 4 * kRowTile + 2 * 1024;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kStageBytes];
+  // LDS: two slots of (Q rows, dO rows) read by S = Q.K^T and dP = dO.V^T, two slots of (Q, dO
+  // transposed-read copies) read by dV and dK, two slots of a tile's 64 lse and 64 D values. Step
+  // i's row tiles are read one step before its transposed tiles: the S / dP MFMAs of step i + 1 run
+  // beside the softmax work of step i, then the dV / dK MFMAs of step i.
+  constexpr int kPair = 2 * kRowTile;
+  constexpr int kRowsOff = 0, kTrOff = 2 * kPair, kRtOff = 4 * kPair;
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kPair + 2 * 2048];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..3
@@ -176,22 +181,36 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   const int per_head = max(0, n_tiles - t0);
   const int n_steps = group * per_head;
 
-  auto stage = [&](int slot, int i) {
-    char *st = smem + slot * kStageBytes;
-    const int h = hk * group + i / per_head, t = t0 + i % per_head;
-    const int valid = a.S_q - t * kBwdQTile;
+  // Staging of step i (clamped to the last step: past the end a slot is refilled, never read
+  // for a result) into the slots given.
+  auto tile_of = [&](int i, int &valid, uint32_t &tb, uint32_t &row_base, int &t) {
+    const int h = hk * group + i / per_head;
+    t = t0 + i % per_head;
+    valid = a.S_q - t * kBwdQTile;
     const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kBD * 2);
-    const uint32_t row_base = (uint32_t)(((size_t)b * a.H + h) * a.S_q) * 4u;
-    const uint32_t tb = qbase + (uint32_t)(t * kBwdQTile) * rs;
+    row_base = (uint32_t)(((size_t)b * a.H + h) * a.S_q) * 4u;
+    tb = qbase + (uint32_t)(t * kBwdQTile) * rs;
+  };
+  auto stage_rows_to = [&](int slot, int i) {
+    char *st = smem + kRowsOff + slot * kPair;
+    int valid, t;
+    uint32_t tb, row_base;
+    tile_of(i, valid, tb, row_base, t);
     stage_rows<4, false>(rq, st, 16 * wave, tb, rs, valid, lane);
-    stage_rows<4, true>(rq, st + kRowTile, 16 * wave, tb, rs, valid, lane);
-    stage_rows<4, false>(rg, st + 2 * kRowTile, 16 * wave, tb, rs, valid, lane);
-    stage_rows<4, true>(rg, st + 3 * kRowTile, 16 * wave, tb, rs, valid, lane);
+    stage_rows<4, false>(rg, st + kRowTile, 16 * wave, tb, rs, valid, lane);
+  };
+  auto stage_tr_to = [&](int slot, int i) {
+    char *st = smem + kTrOff + slot * kPair;
+    int valid, t;
+    uint32_t tb, row_base;
+    tile_of(i, valid, tb, row_base, t);
+    stage_rows<4, true>(rq, st, 16 * wave, tb, rs, valid, lane);
+    stage_rows<4, true>(rg, st + kRowTile, 16 * wave, tb, rs, valid, lane);
     // lse (wave 0) and D (wave 1) of the tile's queries: lanes 0-15 load 4 values each (entries past
     // S_q are never used unmasked); lanes 16-63 write zeros
     if (wave < 2) {
       const uint32_t off = lane < 16 ? row_base + (uint32_t)(t * kBwdQTile + 4 * lane) * 4u : kOOB;
-      lds_direct16(wave == 0 ? rl : rd, st + 4 * kRowTile + wave * 1024, off);
+      lds_direct16(wave == 0 ? rl : rd, smem + kRtOff + slot * 2048 + wave * 1024, off);
     }
   };
 
@@ -204,99 +223,111 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     dv[i] = f32x16{};
   }
 
-  if (n_steps > 0) stage(0, 0);
-  for (int i = 0; i < n_steps; ++i) {
-    wait_vmem();
-    __syncthreads();  // step i's tile is in LDS; everyone is done with step i-1's slot
-    if (i + 1 < n_steps) stage((i + 1) & 1, i + 1);
-    const char *st = smem + (i & 1) * kStageBytes;
-    const char *qrow = st, *qtr = st + kRowTile, *grow = st + 2 * kRowTile, *gtr = st + 3 * kRowTile;
-    const float *lse_t = (const float *)(st + 4 * kRowTile), *d_t = (const float *)(st + 4 * kRowTile + 1024);
-    const int qt0 = (t0 + i % per_head) * kBwdQTile;
-
-    // S and dP for the two 32-query blocks of the tile: 32 MFMAs in four interleaved accumulation
-    // chains (step k: d step k / 4; S of block 0, dP of block 0, S of block 1, dP of block 1), each
-    // operand fragment read MTK_BWD_SDP_AHEAD steps ahead of its MFMA. The fence per step keeps
-    // that order (the scheduler would otherwise regroup the chains and read each fragment just
-    // before its use); every chain still accumulates its d steps in order.
-    f32x16 s[2], p[2];
+  // S and dP of the step whose rows are in rows slot `slot`, for the two 32-query blocks of the
+  // tile: 32 MFMAs in four interleaved accumulation chains (step k: d step k / 4; S of block 0, dP
+  // of block 0, S of block 1, dP of block 1), each operand fragment read MTK_BWD_SDP_AHEAD steps
+  // ahead of its MFMA; after MFMA k, vstep(k) runs one element of the previous step's softmax.
+  // The fence per step keeps that order; every chain still accumulates its d steps in order.
+  auto sdp = [&](int slot, f32x16 (&s_)[2], f32x16 (&p_)[2], auto &&vstep) {
+    const char *qrow = smem + kRowsOff + slot * kPair, *grow = qrow + kRowTile;
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      s[qb] = f32x16{};
-      p[qb] = f32x16{};
+      s_[qb] = f32x16{};
+      p_[qb] = f32x16{};
     }
-    {
-      constexpr int D = MTK_BWD_SDP_AHEAD;
-      auto rd = [&](int k) {
-        const int ds = k >> 2, qb = (k >> 1) & 1;
-        return *(const u32x4 *)(((k & 1) ? grow : qrow) + row_off(32 * qb + arow, 2 * ds + g));
-      };
-      u32x4 fr[D];
+    constexpr int D = MTK_BWD_SDP_AHEAD;
+    auto rdf = [&](int k) {
+      const int ds = k >> 2, qb = (k >> 1) & 1;
+      return *(const u32x4 *)(((k & 1) ? grow : qrow) + row_off(32 * qb + arow, 2 * ds + g));
+    };
+    u32x4 fr[D];
 #pragma unroll
-      for (int k = 0; k < D; ++k) fr[k] = rd(k);
-#pragma unroll
-      for (int k = 0; k < 32; ++k) {
-        __builtin_amdgcn_sched_barrier(0);
-        const int ds = k >> 2, qb = (k >> 1) & 1;
-        if (k & 1)
-          p[qb] = mfma32x32x16<DT>(fr[k % D], vf[ds], p[qb]);
-        else
-          s[qb] = mfma32x32x16<DT>(fr[k % D], kf[ds], s[qb]);
-        if (k + D < 32) fr[k % D] = rd(k + D);
-      }
+    for (int k = 0; k < D; ++k) fr[k] = rdf(k);
+    static_for<0, 32>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
       __builtin_amdgcn_sched_barrier(0);
-    }
+      constexpr int ds = k >> 2, qb = (k >> 1) & 1;
+      if constexpr (k & 1)
+        p_[qb] = mfma32x32x16<DT>(fr[k % D], vf[ds], p_[qb]);
+      else
+        s_[qb] = mfma32x32x16<DT>(fr[k % D], kf[ds], s_[qb]);
+      vstep(kc);
+      if constexpr (k + D < 32) fr[k % D] = rdf(k + D);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+  };
 
-    // P and dS; register r of block qb is query qt0 + 32 qb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8).
-    // Masks only where the tile needs them (this wave's keys past S_kv, queries past S_q, or keys
-    // past the causal diagonal of the tile's first query): elsewhere every element is kept, with
-    // the same bits.
+  f32x16 s[2], p[2];
+  if (n_steps > 0) {
+    stage_rows_to(0, 0);
+    stage_tr_to(0, 0);
+    stage_rows_to(1, min(1, n_steps - 1));
+    wait_vmem();
+    __syncthreads();
+    sdp(0, s, p, [](auto) {});
+  }
+  for (int i = 0; i < n_steps; ++i) {
+    wait_vmem();
+    // rows of step i + 1, transposed tiles and row terms of step i have landed; every wave is done
+    // with the rows of step i, the transposed tiles and row terms of step i - 1
+    __syncthreads();
+    stage_rows_to(i & 1, min(i + 2, n_steps - 1));
+    stage_tr_to((i + 1) & 1, min(i + 1, n_steps - 1));
+    const char *tst = smem + kTrOff + (i & 1) * kPair;
+    const char *qtr = tst, *gtr = tst + kRowTile;
+    const float *lse_t = (const float *)(smem + kRtOff + (i & 1) * 2048), *d_t = lse_t + 256;
+    const int qt0 = (t0 + i % per_head) * kBwdQTile;
+
+    // P and dS of step i; register r of block qb is query qt0 + 32 qb + (r < 8 ? 8 g + r : 16 + 8 g
+    // + r - 8). Masks only where the tile needs them (this wave's keys past S_kv, queries past S_q,
+    // or keys past the causal diagonal of the tile's first query): elsewhere every element is kept,
+    // with the same bits. Element k (qb = k / 16, half = k / 8 % 2, e = k % 8) runs beside MFMA k of
+    // the next step's S / dP.
     const int wave_k_max = k0 + wave * 32 + 31;
     const bool need_mask = wave_k_max >= a.S_kv || qt0 + kBwdQTile > a.S_q || (CAUSAL && wave_k_max > qt0 + diag);
     u32x4 pb[4], sb[4];
-    auto softmax_tile = [&](auto mask_c) {
-    constexpr bool MASK = decltype(mask_c)::value;
+    float pv0 = 0.0f, sv0 = 0.0f;
+    float lse8[8], dd8[8];
+    auto soft = [&](auto mask_c) {
+      constexpr bool MASK = decltype(mask_c)::value;
+      return [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        constexpr int qb = k >> 4, half = (k >> 3) & 1, e = k & 7;
+        constexpr int qr = 32 * qb + 16 * half;  // + 8 g: first of this lane's 8 queries
+        if constexpr (e == 0) {
+          const f32x4 l0 = *(const f32x4 *)(lse_t + qr + 8 * g), l1 = *(const f32x4 *)(lse_t + qr + 8 * g + 4);
+          const f32x4 d0 = *(const f32x4 *)(d_t + qr + 8 * g), d1 = *(const f32x4 *)(d_t + qr + 8 * g + 4);
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int qr = 32 * qb + 16 * half + 8 * g;  // first of 8 consecutive queries of the tile
-        const int q = qt0 + qr;
-        float lse[8], dd[8];
-        {
-          const f32x4 l0 = *(const f32x4 *)(lse_t + qr), l1 = *(const f32x4 *)(lse_t + qr + 4);
-          const f32x4 d0 = *(const f32x4 *)(d_t + qr), d1 = *(const f32x4 *)(d_t + qr + 4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            lse[e] = l0[e];
-            lse[4 + e] = l1[e];
-            dd[e] = d0[e];
-            dd[4 + e] = d1[e];
+          for (int x = 0; x < 4; ++x) {
+            lse8[x] = l0[x];
+            lse8[4 + x] = l1[x];
+            dd8[x] = d0[x];
+            dd8[4 + x] = d1[x];
           }
         }
-        float pv[8], sv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int r = 8 * half + e;
-          const int qi = q + e;
-          const bool ok = !MASK || (key_ok && qi < a.S_q && (!CAUSAL || key <= qi + diag));
-          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][r], c, -lse[e]));
-          pv[e] = ok ? pe : 0.0f;
-          sv[e] = ok ? pe * __builtin_fmaf(p[qb][r], a.scale, -dd[e]) : 0.0f;
+        const float lse_e = lse8[e], dd_e = dd8[e];
+        constexpr int r = 8 * half + e;
+        const int qi = qt0 + qr + 8 * g + e;
+        const bool ok = !MASK || (key_ok && qi < a.S_q && (!CAUSAL || key <= qi + diag));
+        const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][r], c, -lse_e));
+        const float pv = ok ? pe : 0.0f;
+        const float sv = ok ? pe * __builtin_fmaf(p[qb][r], a.scale, -dd_e) : 0.0f;
+        if constexpr (e & 1) {
+          constexpr int js = 2 * qb + half;
+          pb[js][e >> 1] = pack2<DT>(pv0, pv);
+          sb[js][e >> 1] = pack2<DT>(sv0, sv);
+        } else {
+          pv0 = pv;
+          sv0 = sv;
         }
-        const int js = 2 * qb + half;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pb[js][e] = pack2<DT>(pv[2 * e], pv[2 * e + 1]);
-          sb[js][e] = pack2<DT>(sv[2 * e], sv[2 * e + 1]);
-        }
-      }
-    }
+      };
     };
+    f32x16 s2[2], p2[2];
+    const int nslot = (i + 1) & 1;  // past the last step: rows of no step (never used)
     if (need_mask)
-      softmax_tile(std::true_type{});
+      sdp(nslot, s2, p2, soft(std::true_type{}));
     else
-      softmax_tile(std::false_type{});
+      sdp(nslot, s2, p2, soft(std::false_type{}));
 
     // dV^T += dO^T . P and dK^T += Q^T . dS: 32 MFMAs in eight interleaved accumulation chains
     // (step k: 16-query step js = k / 8, d block (k / 2) % 4, dV for even k, dK for odd k), each
@@ -311,11 +342,11 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
         tb[2 * db + 1] = tr_base(qtr, db, lane);
       }
       u32x4 tf[D];
-      auto rd = [&](auto kc) {
+      auto rdt = [&](auto kc) {
         constexpr int K = decltype(kc)::value;
         tf[K % D] = tr_frag<K / 8>(tb[K & 7]);
       };
-      static_for<0, D>([&](auto kc) { rd(kc); });
+      static_for<0, D>([&](auto kc) { rdt(kc); });
       static_for<0, 32>([&](auto kc) {
         constexpr int K = decltype(kc)::value;
         constexpr int kAfter = (31 - K) < (D - 1) ? (31 - K) : (D - 1);  // fragments read after K
@@ -326,9 +357,14 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
           dk[db] = mfma32x32x16<DT>(tf[K % D], sb[js], dk[db]);
         else
           dv[db] = mfma32x32x16<DT>(tf[K % D], pb[js], dv[db]);
-        if constexpr (K + D < 32) rd(std::integral_constant<int, K + D>{});
+        if constexpr (K + D < 32) rdt(std::integral_constant<int, K + D>{});
       });
       __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      s[qb] = s2[qb];
+      p[qb] = p2[qb];
     }
   }
 
