@@ -147,8 +147,7 @@ struct OpConv {
     lds_direct16(r, lds + (blk0 + q) * 1024, ok ? (uint32_t)(pb8[q] + tp.elems) * 2u : kOOB);
   }
   __device__ __forceinline__ u32x4 frag(const char *lds, int rowblk, int ks, int lane) const {
-    // a plain LDS read: the convolution pipeline waits for every read before each k-step
-    return *(const u32x4 *)(lds + lds_off(rowblk + (lane & 31), 2 * ks + (lane >> 5)));
+    return ds_read_b128_at<0>(lds_addr(lds) + lds_off(rowblk + (lane & 31), 2 * ks + (lane >> 5)));
   }
 };
 
@@ -327,7 +326,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   constexpr int kSlotStores = TM * TN * 4;  // slot store instructions per wavefront and boundary
   static_assert(!SERIAL || kSlotStores < 64, "vmcnt range");
 
-  if constexpr (!AOP::kIsConv) {
+  if constexpr (!AOP::kIsConv || BM == 128) {
     // Fragments: a ring of four k-step buffers (slot s holds k-step s of a K-tile), read two k-steps
     // ahead. The reads are inline asm, which the compiler does not track: it would otherwise make
     // every LDS read wait for the direct-to-LDS loads in flight, and at the loop's back edge for
@@ -520,10 +519,10 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       }
     }
   } else {
-    // Convolution: fragments one k-step ahead (two buffers); the loads of K-tile kt + 1 go out in
-    // the first MFMA groups of K-tile kt and are waited for at one barrier before its last k-step.
-    // (The two-ahead ring measured 2-5 % slower on the gather: its loads of K-tile kt + 2 come in
-    // the second half of K-tile kt.)
+    // 256x256 convolution: fragments one k-step ahead (two buffers); the loads of K-tile kt + 1 go
+    // out in the first MFMA groups of K-tile kt and are waited for at one barrier before its last
+    // k-step. (The two-ahead ring measured 2-5 % slower on this gather, whose loads of K-tile kt + 2
+    // then come in the second half of K-tile kt; on the 128x128 convolution it is 1-2 % faster.)
     static_assert(!SERIAL && !kAnyTail, "convolutions never split K and have whole K-tiles");
     constexpr int kGroups1 = (kBK / 16) * TM;
     constexpr int kLoadGroups1 = 8 < kGroups1 - TM ? 8 : kGroups1 - TM;
@@ -554,9 +553,8 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
           wait_vmem();
           __syncthreads();
         }
-        // this k-step's B fragments, read by inline asm one k-step earlier (the plain A reads are
-        // waited for by the compiler)
-        lgkm_wait0(gb[c]);
+        // this k-step's fragments, read by inline asm one k-step earlier
+        frag_wait<0>(ga[c], gb[c]);
         const char *ra_ = ks < kLast ? sa : nxt;
         const char *rb_ = ks < kLast ? sb : nxt + BM * 128;
         const int ksn = ks < kLast ? ks + 1 : 0;
@@ -585,7 +583,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       }
     }
     // the last prefetch (of a K-tile never computed) may still be in flight
-    lgkm_wait0(gb[0]);
+    frag_wait<0>(ga[0], gb[0]);
   }
 
   // ---- epilogue. 32x32 accumulator layout: lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4,
