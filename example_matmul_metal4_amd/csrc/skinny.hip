@@ -67,6 +67,14 @@ struct SkinnyWave {
   }
 };
 
+// Workgroup barrier over LDS data only: this wavefront's LDS operations have completed
+// (lgkmcnt(0)); its global loads stay in flight (__syncthreads' fence would wait for them, which
+// drains the B stream at every reduction).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // Partition results of one group are in LDS; after the barrier the workgroup (64 * split_k
 // threads) sums them for the 256 outputs of the group.
 template <int DT>
@@ -92,6 +100,11 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   constexpr int kStreamPolicy = 2;
   __shared__ __attribute__((aligned(16))) float red[R][8][256];
   __shared__ __attribute__((aligned(16))) u32x4 tr[8][KS][64];  // per wavefront: 16 rows x 64 chunks
+  // the workgroup's bias values, read once before the B stream starts: a global bias load in a
+  // reduction would be the youngest vector-memory operation, and waiting for it (vmcnt(0)) would
+  // also wait for the next group's B loads in flight
+  constexpr int kBiasCache = 4096;
+  __shared__ uint16_t bias_s[kBiasCache];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
@@ -106,16 +119,10 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   const bool k_ok = kl < k_end;
   const int r = lane & 15, q = lane >> 4;
   u32x4(&t)[KS][64] = tr[w];
-
-  // A: row s (s < M) -> slot lane ^ s, fragments read back once
-  u32x4 a[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s)
-    a[s] = buf_load16(ra, (k_ok && s < p.M) ? (uint32_t)s * (uint32_t)p.lda * 2u + (uint32_t)kl * 2u : kOOB);
-#pragma unroll
-  for (int s = 0; s < KS; ++s) t[s][lane ^ s] = a[s];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) a[s] = t[r][(4 * s + q) ^ r];
+  const bool bias_cached = per <= kBiasCache;
+  if (p.has_bias && bias_cached) {
+    for (int i = tid; i < c1 - c0; i += (int)blockDim.x) bias_s[i] = ((const uint16_t *)p.bias)[c0 + i];
+  }
 
   auto load_b = [&](u32x4 (&b)[KS], int col) {
 #pragma unroll
@@ -125,6 +132,18 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
           rb, (k_ok && n < c1) ? (uint32_t)n * (uint32_t)p.ldb * 2u + (uint32_t)kl * 2u : kOOB, 0, kStreamPolicy);
     }
   };
+
+  // A: row s (s < M) -> slot lane ^ s, fragments read back once. The first B group's loads go out
+  // before the transpose waits for A, so the B stream starts at once.
+  u32x4 a[KS], b0[KS], b1[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+    a[s] = buf_load16(ra, (k_ok && s < p.M) ? (uint32_t)s * (uint32_t)p.lda * 2u + (uint32_t)kl * 2u : kOOB);
+  load_b(b0, c0);
+#pragma unroll
+  for (int s = 0; s < KS; ++s) t[s][lane ^ s] = a[s];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) a[s] = t[r][(4 * s + q) ^ r];
   // LDS operations of one wavefront execute in order: the parking writes of a group follow the
   // fragment reads of the previous one.
   auto mma = [&](const u32x4 (&b)[KS]) {
@@ -142,28 +161,29 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   };
   // groups g0 .. g0 + n - 1 are parked in slots 0 .. n - 1
   auto flush = [&](int g0, int n) {
-    __syncthreads();
+    lds_barrier();
     for (int e = tid; e < n * 256; e += (int)blockDim.x) {
       const int sl = e >> 8, o = e & 255, m = o >> 4;
       const int col = c0 + 16 * (g0 + sl) + (o & 15);
       float sum = red[sl][0][o];
       for (int ww = 1; ww < p.split_k; ++ww) sum += red[sl][ww][o];
       if (m < p.M && col < c1) {
-        if (p.has_bias) sum += from_bits<DT>(((const uint16_t *)p.bias)[col]);
+        if (p.has_bias) sum += from_bits<DT>(bias_cached ? bias_s[col - c0] : ((const uint16_t *)p.bias)[col]);
         ((uint16_t *)p.C)[(size_t)m * p.ldc + col] = to_bits<DT>(sum);
       }
     }
-    __syncthreads();
+    lds_barrier();
   };
 
-  u32x4 b0[KS], b1[KS];
-  if (ng > 0) load_b(b0, c0);
+  // The next group's loads are issued unconditionally (columns past c1 read zeros without touching
+  // memory): with a branch around them the compiler's wait before each park would have to assume
+  // either path and waits for the next group's loads as well, which serializes the stream.
   for (int g = 0; g < ng; g += 2) {
-    if (g + 1 < ng) load_b(b1, c0 + 16 * (g + 1));
+    load_b(b1, c0 + 16 * (g + 1));
     park(g % R, mma(b0));
     if (g % R == R - 1 || g + 1 == ng) flush(g - g % R, g % R + 1);
     if (g + 1 >= ng) break;
-    if (g + 2 < ng) load_b(b0, c0 + 16 * (g + 2));
+    load_b(b0, c0 + 16 * (g + 2));
     park((g + 1) % R, mma(b1));
     if ((g + 1) % R == R - 1 || g + 2 == ng) flush(g + 1 - (g + 1) % R, (g + 1) % R + 1);
   }
@@ -202,7 +222,7 @@ __device__ __forceinline__ void skinny_gemm_long(const mtk_skinny_args &p) {
       acc = sw.mma(b, acc);
     }
     park(buf, acc);
-    __syncthreads();
+    lds_barrier();
     skinny_reduce_store<DT>(p, red[buf], g, tid);
     buf ^= 1;
   }
@@ -293,8 +313,7 @@ __device__ __forceinline__ void skinny_gemm_parts(const mtk_skinny_args &p) {
   // past the partition read zeros), so the compiler's waits for each register buffer are exact.
   auto step = [&](int j, const u32x4 (&ac)[4], const u32x4 (&bc)[8], int buf, u32x4 (&an)[4], u32x4 (&bn)[8]) {
     store_a(ac, buf);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    asm volatile("s_barrier" ::: "memory");
+    lds_barrier();
     load_a(an, k0 + 32 * KS * (j + 2));
     load_b(bn, k0 + 32 * KS * (j + 2));
     mma(bc, buf);
