@@ -145,7 +145,7 @@ def cpu_baseline(target_s=10.0):
 
 
 def cpu_baselines_other(target_s=3.0):
-    """The CPU oracle on bounded samples of the other MFMA-bound configs:
+    """The CPU oracle on bounded samples of the other MFMA-bound configurations:
     attention (config 5, Network.swift:134-179 / 286-311 restated) on a block of query rows of
     every (b, h), conv2d (config 4a, ConvolutionShared.swift:4994-5026) on a block of output rows.
     Each sample grows until it takes about target_s seconds; TFLOP/s counts the sampled work."""
