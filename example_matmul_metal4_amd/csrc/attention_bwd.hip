@@ -67,6 +67,12 @@ __device__ __forceinline__ u32x4 tr_frag(uint32_t base) {
 #ifndef MTK_BWD_SDP_AHEAD
 #define MTK_BWD_SDP_AHEAD 8
 #endif
+#ifndef MTK_DQ_SDP_AHEAD
+#define MTK_DQ_SDP_AHEAD 4
+#endif
+#ifndef MTK_DQ_TR_AHEAD
+#define MTK_DQ_TR_AHEAD 4
+#endif
 #ifndef MTK_BWD_TR_AHEAD
 #define MTK_BWD_TR_AHEAD 8
 #endif
@@ -288,9 +294,10 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     u32x4 pb[4], sb[4];
     float pv0 = 0.0f, sv0 = 0.0f;
     float lse8[8], dd8[8];
+    // the returned element step takes the mask choice by value (nothing of this call's frame)
     auto soft = [&](auto mask_c) {
-      constexpr bool MASK = decltype(mask_c)::value;
-      return [&](auto kc) {
+      return [&, mask_c](auto kc) {
+        constexpr bool MASK = decltype(mask_c)::value;
         constexpr int k = decltype(kc)::value;
         constexpr int qb = k >> 4, half = (k >> 3) & 1, e = k & 7;
         constexpr int qr = 32 * qb + 16 * half;  // + 8 g: first of this lane's 8 queries
@@ -474,63 +481,86 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
     const char *krow = st, *ktr = st + kRowTile, *vrow = st + 2 * kRowTile;
     const int j0 = t * kBwdKTile;
 
-    // S^T and dP^T for the two 32-key blocks of the tile
-    f32x16 s[2], p[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = f32x16{};
-      p[kb] = f32x16{};
-#pragma unroll
-      for (int ds = 0; ds < 8; ++ds) {
-        const uint32_t o = row_off(32 * kb + arow, 2 * ds + g);
-        s[kb] = mfma32x32x16<DT>(*(const u32x4 *)(krow + o), qf[ds], s[kb]);
-        p[kb] = mfma32x32x16<DT>(*(const u32x4 *)(vrow + o), gf[ds], p[kb]);
-      }
-    }
-
-    // dS^T; register r of block kb is key j0 + 32 kb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8). Masks
-    // only where the tile needs them (as in the dK/dV kernel).
+    // The tile in two halves of 32 keys (kb = 0, 1): S^T and dP^T of the half, its dS^T, then the
+    // dQ MFMAs of its two 16-key steps. Per d block dQ still accumulates the tile's key steps in
+    // order (the same bits as a whole tile at once); half a tile of scores leaves the registers for
+    // operand fragments read ahead (read just before its MFMA, every fragment waited for its read).
     const int wave_q0 = q0 + wave * 32;
     const bool need_mask = wave_q0 + 31 >= a.S_q || j0 + kBwdKTile > a.S_kv || (CAUSAL && j0 + kBwdKTile - 1 > wave_q0 + diag);
-    u32x4 sb[4];
-    auto softmax_tile = [&](auto mask_c) {
-    constexpr bool MASK = decltype(mask_c)::value;
+    static_for<0, 2>([&](auto kc) {
+      constexpr int kb = decltype(kc)::value;
+      // S^T and dP^T: 16 MFMAs in two chains (step k: d step k / 2, S for even k, dP for odd k),
+      // each fragment read MTK_DQ_SDP_AHEAD steps ahead; the fence per step keeps that order
+      f32x16 s = f32x16{}, p = f32x16{};
+      {
+        constexpr int D = MTK_DQ_SDP_AHEAD;
+        auto rdf = [&](int k) {
+          return *(const u32x4 *)(((k & 1) ? vrow : krow) + row_off(32 * kb + arow, 2 * (k >> 1) + g));
+        };
+        u32x4 fr[D];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+        for (int k = 0; k < D; ++k) fr[k] = rdf(k);
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        float sv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int r = 8 * half + e;
-          const int kj = j0 + 32 * kb + 16 * half + 8 * g + e;
-          const bool ok = !MASK || (q_ok && kj < a.S_kv && (!CAUSAL || kj <= qi + diag));
-          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], c, -lse2));
-          sv[e] = ok ? pe * __builtin_fmaf(p[kb][r], a.scale, -dterm) : 0.0f;
+        for (int k = 0; k < 16; ++k) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (k & 1)
+            p = mfma32x32x16<DT>(fr[k % D], gf[k >> 1], p);
+          else
+            s = mfma32x32x16<DT>(fr[k % D], qf[k >> 1], s);
+          if (k + D < 16) fr[k % D] = rdf(k + D);
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sb[2 * kb + half][e] = pack2<DT>(sv[2 * e], sv[2 * e + 1]);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    }
-    };
-    if (need_mask)
-      softmax_tile(std::true_type{});
-    else
-      softmax_tile(std::false_type{});
 
-    // dQ^T += K^T . dS^T, d block by d block
+      // dS^T; register r is key j0 + 32 kb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8). Masks only where
+      // the tile needs them (as in the dK/dV kernel).
+      u32x4 sb[2];
+      auto softmax_half = [&](auto mask_c) {
+        constexpr bool MASK = decltype(mask_c)::value;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const uint32_t kbase_ = tr_base(ktr, db, lane);
-      u32x4 kt[4];
-      static_for<0, 4>([&](auto jc) {
-        constexpr int JS = decltype(jc)::value;
-        kt[JS] = tr_frag<JS>(kbase_);
-      });
-      lgkm_wait0(kt);
+        for (int half = 0; half < 2; ++half) {
+          float sv[8];
 #pragma unroll
-      for (int js = 0; js < 4; ++js) dq[db] = mfma32x32x16<DT>(kt[js], sb[js], dq[db]);
-    }
+          for (int e = 0; e < 8; ++e) {
+            const int r = 8 * half + e;
+            const int kj = j0 + 32 * kb + 16 * half + 8 * g + e;
+            const bool ok = !MASK || (q_ok && kj < a.S_kv && (!CAUSAL || kj <= qi + diag));
+            const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -lse2));
+            sv[e] = ok ? pe * __builtin_fmaf(p[r], a.scale, -dterm) : 0.0f;
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sb[half][e] = pack2<DT>(sv[2 * e], sv[2 * e + 1]);
+        }
+      };
+      if (need_mask)
+        softmax_half(std::true_type{});
+      else
+        softmax_half(std::false_type{});
+
+      // dQ^T += K^T . dS^T for key steps 2 kb, 2 kb + 1: 8 MFMAs (step K: d block K / 2, key step
+      // 2 kb + K % 2), each transposed fragment read MTK_DQ_TR_AHEAD steps ahead
+      {
+        constexpr int D = MTK_DQ_TR_AHEAD;
+        uint32_t tb[4];
+#pragma unroll
+        for (int db = 0; db < 4; ++db) tb[db] = tr_base(ktr, db, lane);
+        u32x4 tf[D];
+        auto rdt = [&](auto kc2) {
+          constexpr int K = decltype(kc2)::value;
+          tf[K % D] = tr_frag<2 * kb + (K & 1)>(tb[K >> 1]);
+        };
+        static_for<0, D>([&](auto kc2) { rdt(kc2); });
+        static_for<0, 8>([&](auto kc2) {
+          constexpr int K = decltype(kc2)::value;
+          constexpr int kAfter = (7 - K) < (D - 1) ? (7 - K) : (D - 1);  // fragments read after K
+          __builtin_amdgcn_sched_barrier(0);
+          lgkm_wait_n<2 * kAfter>(tf[K % D]);
+          dq[K >> 1] = mfma32x32x16<DT>(tf[K % D], sb[K & 1], dq[K >> 1]);
+          if constexpr (K + D < 8) rdt(std::integral_constant<int, K + D>{});
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    });
   }
 
   // dQ[qi][d]: lane = query, register 4 rq + e of block db = d 32 db + 8 rq + 4 g + e; parked in
