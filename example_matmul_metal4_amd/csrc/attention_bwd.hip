@@ -67,6 +67,11 @@ __device__ __forceinline__ u32x4 tr_frag(uint32_t base) {
 #ifndef MTK_BWD_SDP_AHEAD
 #define MTK_BWD_SDP_AHEAD 8
 #endif
+// Wave issue priority over the MFMA sections of the dQ kernel (the two wavefronts of a SIMD: the
+// one in an MFMA section issues first). Causal 3 % faster, non-causal unchanged.
+#ifndef MTK_DQ_PRIO
+#define MTK_DQ_PRIO 1
+#endif
 #ifndef MTK_DQ_SDP_AHEAD
 #define MTK_DQ_SDP_AHEAD 4
 #endif
@@ -498,6 +503,7 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
           return *(const u32x4 *)(((k & 1) ? vrow : krow) + row_off(32 * kb + arow, 2 * (k >> 1) + g));
         };
         u32x4 fr[D];
+        if constexpr (MTK_DQ_PRIO != 0) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int k = 0; k < D; ++k) fr[k] = rdf(k);
 #pragma unroll
@@ -510,6 +516,7 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
           if (k + D < 16) fr[k % D] = rdf(k + D);
         }
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (MTK_DQ_PRIO != 0) __builtin_amdgcn_s_setprio(0);
       }
 
       // dS^T; register r is key j0 + 32 kb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8). Masks only where
@@ -550,6 +557,7 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
           tf[K % D] = tr_frag<2 * kb + (K & 1)>(tb[K >> 1]);
         };
         static_for<0, D>([&](auto kc2) { rdt(kc2); });
+        if constexpr (MTK_DQ_PRIO != 0) __builtin_amdgcn_s_setprio(1);
         static_for<0, 8>([&](auto kc2) {
           constexpr int K = decltype(kc2)::value;
           constexpr int kAfter = (7 - K) < (D - 1) ? (7 - K) : (D - 1);  // fragments read after K
@@ -559,6 +567,7 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
           if constexpr (K + D < 8) rdt(std::integral_constant<int, K + D>{});
         });
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (MTK_DQ_PRIO != 0) __builtin_amdgcn_s_setprio(0);
       }
     });
   }
