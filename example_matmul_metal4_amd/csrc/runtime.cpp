@@ -760,13 +760,14 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   const bool gen = d.D % 8 != 0;
   p->align_a = p->align_b = gen ? 2 : 16;
   // Query rows per workgroup: 256 (the ping-pong kernel: 8 wavefronts in two groups alternating MFMA
-  // and softmax blocks, one workgroup per CU) when its grid still fills the device, causal or not
-  // (config 5 causal, one box: 299 us against 316 us for 128 rows, with the kernels' balanced
-  // causal dispatch order); 128 (4 wavefronts, two workgroups per CU) otherwise.
+  // and softmax blocks, one workgroup per CU) for non-causal D = 128 grids that still fill the device
+  // (config 5, one box: 526.5 us against 546.5 us for 128 rows); 128 (4 wavefronts, two workgroups
+  // per CU) otherwise, causal included (config 5 causal, one box: 298.7 us against 305.3 us for the
+  // ping-pong kernel, both in the kernels' balanced causal dispatch order).
   int rows = d.q_rows;
   if (rows == 0) {
     const int cus = ctx ? ctx->prop.multiProcessorCount : 256;
-    rows = (d.D == 128 && (long long)d.B * d.H * ((d.S_q + 255) / 256) >= cus) ? 256 : 128;
+    rows = (d.D == 128 && !d.causal && (long long)d.B * d.H * ((d.S_q + 255) / 256) >= cus) ? 256 : 128;
   }
   Launch g;
   std::string family = rows == 256 ? "pp_" : "";

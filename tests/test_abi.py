@@ -275,11 +275,11 @@ def test_conv_descriptor_validation(field, value, status):
 
 
 def test_attention_select_and_validation():
-    # config 5, causal or not -> the 256-row ping-pong kernel; 128 rows on request
+    # config 5 -> the 256-row ping-pong kernel, causal -> 128 rows; either on request
     p = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128, causal=True)
-    assert p.describe().endswith("kernels: mtk_attn_fwd_pp_f16_causal") and "rows/wg=256 grid=1024" in p.describe()
-    p = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128, causal=True, q_rows=128)
     assert p.describe().endswith("kernels: mtk_attn_fwd_f16_causal") and "rows/wg=128 grid=2048" in p.describe()
+    pc = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128, causal=True, q_rows=256)
+    assert pc.describe().endswith("kernels: mtk_attn_fwd_pp_f16_causal") and "rows/wg=256 grid=1024" in pc.describe()
     p256 = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128)
     assert p256.describe().endswith("kernels: mtk_attn_fwd_pp_f16") and "rows/wg=256 grid=1024" in p256.describe()
     assert mtk.AttentionPlan(None, 2, 32, 4096, 4096, 128, q_rows=128).describe().endswith("kernels: mtk_attn_fwd_f16")
