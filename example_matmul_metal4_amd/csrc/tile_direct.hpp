@@ -211,7 +211,7 @@ __device__ __forceinline__ void vm_wait() {
 // the two wavefronts of a SIMD belong to different workgroups and drift apart): the one in its
 // MFMA groups issues first, the other's loads and reads fill the gaps. 128x128 convolution 3 %
 // faster; the 256x256 tiles (both wavefronts of a SIMD in one workgroup, in step at its barriers)
-// measured no gain. MTK_KSTEP_PRIO=0 builds without it.
+// measured no gain per k-step and 2-3 % slower per MFMA group. MTK_KSTEP_PRIO=0 builds without it.
 #ifndef MTK_KSTEP_PRIO
 #define MTK_KSTEP_PRIO 1
 #endif
