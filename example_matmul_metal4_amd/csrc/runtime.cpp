@@ -639,7 +639,10 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
       bm = 128;
       bn = 128;
     }
-    if ((M + bm - 1) / bm * ((d.O + bn - 1) / bn) < 128) bm = bn = 128;
+    // Fewer than ~140 tiles of 256x256: 128x128 at two workgroups per CU (one box: 128 tiles,
+    // conv2d 2x128x128x256 3x3, 66.2 us on 256x256 against 51.3 us; 144 tiles 124.4 against
+    // 140.4 us; 192 tiles 72.4 against 82.5 us).
+    if ((M + bm - 1) / bm * ((d.O + bn - 1) / bn) < 140) bm = bn = 128;
   } else {
     va = direct_oidhw ? pow2_vec({d.C}) : pow2_vec({d.C, d.O});
     bm = bn = 128;
