@@ -90,27 +90,42 @@ def gemm_case(dev, mtk, inputs, M, N, K, dtype, split_k, seeds, dists, copies=3,
 
 
 def summarize(name, plan, timing, bound, key=None):
+    """One configuration's line. Kernel rates use the sum of the plan's per-step kernel times (every
+    kernel of a multi-kernel plan, each averaged over the profiled launches), so they cover the
+    whole step's work. HIP event pairs around a launch add a few microseconds of their own, so when
+    that sum exceeds the graph's wall time per step (short kernels), the graph time is used."""
     wall_ms, eager_ms, prof = timing
     flops, byts = plan.work()
     kern = max(prof["kernels"].items(), key=lambda kv: kv[1])
+    events_ms = sum(prof["kernels"].values())
+    kernel_ms, source = (events_ms, "HIP events, sum over the plan's kernels") if events_ms <= wall_ms else (
+        wall_ms, "graph wall time per step (the event-timed sum exceeds it)")
     out = {"workload": name, "plan": plan.describe(), "ms_per_step": wall_ms, "eager_ms_per_step": eager_ms,
            "tflops": flops / (wall_ms * 1e-3) / 1e12, "pct_mfma_peak": 100 * flops / (wall_ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS,
-           "kernels_ms": prof["kernels"], "dominant_kernel": kern[0],
-           "traffic": traffic_for(f"{kern[0]}@{key}") if key else None}
+           "kernels_ms": prof["kernels"], "kernels_total_ms": kernel_ms, "kernel_time_source": source,
+           "dominant_kernel": kern[0], "traffic": traffic_for(f"{kern[0]}@{key}") if key else None}
     if bound == "hbm":
         out["gbs"] = byts / (wall_ms * 1e-3) / 1e9
         out["pct_hbm_peak"] = 100 * out["gbs"] / PEAK_HBM_GBS
-        out["kernel_gbs"] = byts / (kern[1] * 1e-3) / 1e9
+        out["kernel_gbs"] = byts / (kernel_ms * 1e-3) / 1e9
     else:
-        out["kernel_tflops"] = flops / (kern[1] * 1e-3) / 1e12
+        out["kernel_tflops"] = flops / (kernel_ms * 1e-3) / 1e12
     return out
+
+
+def host_threads():
+    """Host threads for the CPU baselines: every CPU this process may run on, capped by
+    OMP_NUM_THREADS when the environment sets it (the GPU box sets it to its CPU share per GPU)."""
+    cpus = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return (min(cpus, int(env)) if env.isdigit() and int(env) > 0 else cpus), cpus
 
 
 def cpu_baseline(target_s=10.0):
     """Oracle GEMM (config 2 shape) on a growing row sample until ~target_s of CPU work."""
     import oracle
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads, cpus = host_threads()
     M, N, K = 4096, 4096, 4100
     B = oracle.normal(2, (N, K), 0, 1 / np.sqrt(K))
     bias = oracle.uniform(3, (N,), -0.5, 0.5)
@@ -138,10 +153,12 @@ def cpu_baseline(target_s=10.0):
                 break
     except OSError:
         pass
-    return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+    return {"value": tflops, "unit": "TFLOP/s", "cores": threads, "host_cpus": cpus,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "kind": "port",
             "sample": f"oracle_gemm (fp32 sequential accumulate, matmul.swift:498-510) on {rows} of the 4096 rows "
                       f"of config 2 (M=N=4096, K=4100, bias), {el:.2f} s per run averaged over {reps} run(s), "
-                      f"{threads} threads of {cpu}"}
+                      f"{threads} threads ({cpus} CPUs in this process's affinity, OMP_NUM_THREADS="
+                      f"{os.environ.get('OMP_NUM_THREADS')}) of {cpu}"}
 
 
 def cpu_baselines_other(target_s=3.0):
@@ -151,7 +168,7 @@ def cpu_baselines_other(target_s=3.0):
     Each sample grows until it takes about target_s seconds; TFLOP/s counts the sampled work."""
     import oracle
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads, _ = host_threads()
     out = {}
     Q = oracle.normal(10, (2, 4096, 32, 128))
     K = oracle.normal(11, (2, 4096, 32, 128))
@@ -348,16 +365,6 @@ def main():
                     s["reference_m5_tflops"] = 9.07
                     s["overhead_vs_dhwio_pct"] = 100.0 * (tm[0] / cfgs[key]["ms_per_step"] - 1.0)
                     cfgs["reference_profile_permute_conv3d"] = s
-                    # the permutation fused into the convolution's weight staging instead: the same
-                    # OIDHW weights read in place (one kernel, no workspace, 2-byte weight gathers)
-                    desc.weight_layout = mtk.WEIGHTS_OIDHW_DIRECT
-                    pd = mtk.ConvPlan(dev, desc)
-                    sets_d = [pd.args(sf.x, sf.w, None, y) for sf in sets_f]
-                    tm = time_steps(dev, pd, sets_d, args.warmup, steps)
-                    s = summarize(pd.describe().split(" kernels:")[0], pd, tm, "mfma",
-                                  key="reference_profile_oidhw_direct_conv3d")
-                    s["vs_two_pass_permute_conv"] = tm[0] / cfgs["reference_profile_permute_conv3d"]["ms_per_step"]
-                    cfgs["reference_profile_oidhw_direct_conv3d"] = s
             # OIDHW -> DHWIO weight re-layout at the reference's profile shape (512 x 512, 3x3x3;
             # AGENTS.md:51), HBM-bound: 40 rotating source copies (566 MB with the destination) so the
             # 256 MB Infinity Cache cannot serve the repeats

@@ -487,8 +487,8 @@ def permute_oidhw_to_dhwio(dev: Device, w) -> np.ndarray:
     return out
 
 
-WEIGHTS_DHWIO, WEIGHTS_OIDHW, WEIGHTS_OIDHW_DIRECT = 0, 1, 2
-_WEIGHT_LAYOUTS = {"DHWIO": WEIGHTS_DHWIO, "OIDHW": WEIGHTS_OIDHW, "OIDHW_DIRECT": WEIGHTS_OIDHW_DIRECT}
+WEIGHTS_DHWIO, WEIGHTS_OIDHW = 0, 1
+_WEIGHT_LAYOUTS = {"DHWIO": WEIGHTS_DHWIO, "OIDHW": WEIGHTS_OIDHW}
 
 
 def conv_desc(dims, has_bias=False, rank=None, weight_layout="DHWIO") -> ConvDesc:
@@ -496,8 +496,7 @@ def conv_desc(dims, has_bias=False, rank=None, weight_layout="DHWIO") -> ConvDes
 
     rank defaults to 2 when the depth axis is trivial (D = KD = 1, no depth padding), else 3.
     weight_layout "OIDHW": the weights are [O][C][KD][KH][KW] and each run re-lays them out in the
-    plan's workspace first (the reference's PermuteThenTensorOpSession3D); "OIDHW_DIRECT": the same
-    weights read in place by the convolution's weight staging (one kernel, no workspace, slower)."""
+    plan's workspace first (the reference's PermuteThenTensorOpSession3D)."""
     g = (lambda k, dflt=0: getattr(dims, k, dflt))
     if rank is None:
         rank = 2 if (g("D", 1) == 1 and g("KD", 1) == 1 and not g("PF") and not g("PBk")) else 3
@@ -597,7 +596,7 @@ def attention_bwd(dev: Device, Q, K, V, O, dO, lse, *, causal=False, dtype="f16"
 def conv(dev: Device, dims, x, w, bias=None, *, weight_layout="DHWIO") -> np.ndarray:
     """TensorOpSession*.run equivalent: one implicit-GEMM launch; returns the f16 output. With
     weight_layout "OIDHW", w is [O][C][KD][KH][KW] (rank 2: [O][C][KH][KW]) and the run re-lays it
-    out first (PermuteThenTensorOpSession3D.run); "OIDHW_DIRECT" reads the same weights in place."""
+    out first (PermuteThenTensorOpSession3D.run)."""
     desc = conv_desc(dims, has_bias=bias is not None, weight_layout=weight_layout)
     plan = ConvPlan(dev, desc)
     shape = plan.out_shape()

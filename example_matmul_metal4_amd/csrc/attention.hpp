@@ -49,9 +49,6 @@
 // Wave issue priority over phase A of the 128-query kernel (S(t+1) MFMAs with the exponentials of
 // tile t): of the two wavefronts of a SIMD (two workgroups per CU, out of step), the one in phase A
 // issues first. 1-2.5 % faster than equal priorities (priority over phase B instead: mixed).
-#ifndef MTK_FWD128_PRIO
-#define MTK_FWD128_PRIO 1
-#endif
 
 namespace mtk {
 
@@ -310,7 +307,7 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
       }
 
       // phase A: S(t+1) MFMAs interleaved with exp / sum / pack of tile t
-      if constexpr (MTK_FWD128_PRIO != 0) __builtin_amdgcn_s_setprio(1);
+      __builtin_amdgcn_s_setprio(1);
       f32x16 n0 = f32x16{}, n1 = f32x16{};
       u32x4 pf[4];
       float psum = 0.0f;
@@ -335,7 +332,7 @@ __device__ __forceinline__ void attn_fwd(const mtk_attn_kargs &a) {
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (MTK_FWD128_PRIO != 0) __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_s_setprio(0);
       l_run += psum;
 
       // phase B: O^T += V^T(t) . P^T(t), interleaved with the row max of S(t+1); the next d

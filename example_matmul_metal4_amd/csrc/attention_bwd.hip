@@ -64,23 +64,14 @@ __device__ __forceinline__ u32x4 tr_frag(uint32_t base) {
   return u32x4{w0.x, w0.y, w1.x, w1.y};
 }
 
-#ifndef MTK_BWD_SDP_AHEAD
-#define MTK_BWD_SDP_AHEAD 8
-#endif
-// Wave issue priority over the MFMA sections of the dQ kernel (the two wavefronts of a SIMD: the
-// one in an MFMA section issues first). Causal 3 % faster, non-causal unchanged.
-#ifndef MTK_DQ_PRIO
-#define MTK_DQ_PRIO 1
-#endif
-#ifndef MTK_DQ_SDP_AHEAD
-#define MTK_DQ_SDP_AHEAD 4
-#endif
-#ifndef MTK_DQ_TR_AHEAD
-#define MTK_DQ_TR_AHEAD 4
-#endif
-#ifndef MTK_BWD_TR_AHEAD
-#define MTK_BWD_TR_AHEAD 8
-#endif
+// Operand fragments read ahead of their MFMAs, in MFMA steps: dK/dV S / dP products and dV / dK
+// products, dQ S^T / dP^T products and dQ products (the measured best of each).
+constexpr int kBwdSdpAhead = 8;
+constexpr int kBwdTrAhead = 8;
+constexpr int kDqSdpAhead = 4;
+constexpr int kDqTrAhead = 4;
+// The dQ kernel's MFMA sections run at raised wave issue priority (of the two wavefronts of a SIMD,
+// the one in an MFMA section issues first): causal 3 % faster, non-causal unchanged.
 // Wait until at most N LDS operations are outstanding; f (filled by an inline-asm read) is handed
 // on through the wait, so its consumers cannot be scheduled above it.
 template <int N>
@@ -236,7 +227,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
 
   // S and dP of the step whose rows are in rows slot `slot`, for the two 32-query blocks of the
   // tile: 32 MFMAs in four interleaved accumulation chains (step k: d step k / 4; S of block 0, dP
-  // of block 0, S of block 1, dP of block 1), each operand fragment read MTK_BWD_SDP_AHEAD steps
+  // of block 0, S of block 1, dP of block 1), each operand fragment read kBwdSdpAhead steps
   // ahead of its MFMA; after MFMA k, vstep(k) runs one element of the previous step's softmax.
   // The fence per step keeps that order; every chain still accumulates its d steps in order.
   auto sdp = [&](int slot, f32x16 (&s_)[2], f32x16 (&p_)[2], auto &&vstep) {
@@ -246,7 +237,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
       s_[qb] = f32x16{};
       p_[qb] = f32x16{};
     }
-    constexpr int D = MTK_BWD_SDP_AHEAD;
+    constexpr int D = kBwdSdpAhead;
     auto rdf = [&](int k) {
       const int ds = k >> 2, qb = (k >> 1) & 1;
       return *(const u32x4 *)(((k & 1) ? grow : qrow) + row_off(32 * qb + arow, 2 * ds + g));
@@ -343,10 +334,10 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
 
     // dV^T += dO^T . P and dK^T += Q^T . dS: 32 MFMAs in eight interleaved accumulation chains
     // (step k: 16-query step js = k / 8, d block (k / 2) % 4, dV for even k, dK for odd k), each
-    // transposed operand fragment read MTK_BWD_TR_AHEAD steps ahead; every dV[db] / dK[db] still
+    // transposed operand fragment read kBwdTrAhead steps ahead; every dV[db] / dK[db] still
     // accumulates js = 0..3 in order.
     {
-      constexpr int D = MTK_BWD_TR_AHEAD;
+      constexpr int D = kBwdTrAhead;
       uint32_t tb[8];
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
@@ -384,6 +375,9 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   // The tiles go through LDS (free after the loop): each wave parks its 32 keys as 256-byte rows
   // (16-byte chunk c of row r at chunk c ^ (r & 15)), then stores whole rows, 16 bytes per lane, so
   // every store instruction writes four complete rows instead of 8-byte pieces of 32 rows.
+  // The last iterations issue clamped loads past the end into the stages; they must have landed
+  // before the stages are reused for the output tiles (explicit, not left to the fence's own wait).
+  wait_vmem();
   __syncthreads();  // every wave is done reading the last stage
   char *pk = smem + wave * (2 * 32 * 256), *pv = pk + 32 * 256;
 #pragma unroll
@@ -495,15 +489,15 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
     static_for<0, 2>([&](auto kc) {
       constexpr int kb = decltype(kc)::value;
       // S^T and dP^T: 16 MFMAs in two chains (step k: d step k / 2, S for even k, dP for odd k),
-      // each fragment read MTK_DQ_SDP_AHEAD steps ahead; the fence per step keeps that order
+      // each fragment read kDqSdpAhead steps ahead; the fence per step keeps that order
       f32x16 s = f32x16{}, p = f32x16{};
       {
-        constexpr int D = MTK_DQ_SDP_AHEAD;
+        constexpr int D = kDqSdpAhead;
         auto rdf = [&](int k) {
           return *(const u32x4 *)(((k & 1) ? vrow : krow) + row_off(32 * kb + arow, 2 * (k >> 1) + g));
         };
         u32x4 fr[D];
-        if constexpr (MTK_DQ_PRIO != 0) __builtin_amdgcn_s_setprio(1);
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int k = 0; k < D; ++k) fr[k] = rdf(k);
 #pragma unroll
@@ -516,7 +510,7 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
           if (k + D < 16) fr[k % D] = rdf(k + D);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (MTK_DQ_PRIO != 0) __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_s_setprio(0);
       }
 
       // dS^T; register r is key j0 + 32 kb + (r < 8 ? 8 g + r : 16 + 8 g + r - 8). Masks only where
@@ -545,9 +539,9 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
         softmax_half(std::false_type{});
 
       // dQ^T += K^T . dS^T for key steps 2 kb, 2 kb + 1: 8 MFMAs (step K: d block K / 2, key step
-      // 2 kb + K % 2), each transposed fragment read MTK_DQ_TR_AHEAD steps ahead
+      // 2 kb + K % 2), each transposed fragment read kDqTrAhead steps ahead
       {
-        constexpr int D = MTK_DQ_TR_AHEAD;
+        constexpr int D = kDqTrAhead;
         uint32_t tb[4];
 #pragma unroll
         for (int db = 0; db < 4; ++db) tb[db] = tr_base(ktr, db, lane);
@@ -557,7 +551,7 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
           tf[K % D] = tr_frag<2 * kb + (K & 1)>(tb[K >> 1]);
         };
         static_for<0, D>([&](auto kc2) { rdt(kc2); });
-        if constexpr (MTK_DQ_PRIO != 0) __builtin_amdgcn_s_setprio(1);
+        __builtin_amdgcn_s_setprio(1);
         static_for<0, 8>([&](auto kc2) {
           constexpr int K = decltype(kc2)::value;
           constexpr int kAfter = (7 - K) < (D - 1) ? (7 - K) : (D - 1);  // fragments read after K
@@ -567,13 +561,14 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
           if constexpr (K + D < 8) rdt(std::integral_constant<int, K + D>{});
         });
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (MTK_DQ_PRIO != 0) __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_s_setprio(0);
       }
     });
   }
 
   // dQ[qi][d]: lane = query, register 4 rq + e of block db = d 32 db + 8 rq + 4 g + e; parked in
-  // LDS as 256-byte rows and stored as whole rows, as in the dK/dV kernel
+  // LDS as 256-byte rows and stored as whole rows, as in the dK/dV kernel (no loads are in flight
+  // here: the loop stages no tile past the last and waits for each tile it staged)
   __syncthreads();  // every wave is done reading the last stage
   char *pq = smem + wave * (32 * 256);
 #pragma unroll

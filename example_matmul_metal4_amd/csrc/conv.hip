@@ -3,7 +3,6 @@
 //   *_fast_*_d  C % 64 == 0: each 64-wide K-tile is one filter tap; direct-to-LDS gather (padding
 //               taps read as zero), weights staged [K][O] and read transposed
 //   *_gen_*_vV  any C: register-staged gather with per-group tap decode, V-wide loads
-//   *_gen_*_vV_oidhw  the same gather, OIDHW weights read in place (2-byte loads)
 #include "tile_direct.hpp"
 
 using namespace mtk;
@@ -26,7 +25,3 @@ DIRECT_KERNEL(mtk_conv_f16_fast_128x128_d, 128, 128, 2, 2)
 TILE_KERNEL(mtk_conv_f16_gen_128x128_v8, DT_F16, 128, 128, 2, 2, A_CONV_GENERIC, B_KN, 8, 8)
 TILE_KERNEL(mtk_conv_f16_gen_128x128_v4, DT_F16, 128, 128, 2, 2, A_CONV_GENERIC, B_KN, 4, 4)
 TILE_KERNEL(mtk_conv_f16_gen_128x128_v1, DT_F16, 128, 128, 2, 2, A_CONV_GENERIC, B_KN, 1, 1)
-// OIDHW weights read in place (no re-layout pass): B gathered element by element
-TILE_KERNEL(mtk_conv_f16_gen_128x128_v8_oidhw, DT_F16, 128, 128, 2, 2, A_CONV_GENERIC, B_OIDHW, 8, 1)
-TILE_KERNEL(mtk_conv_f16_gen_128x128_v4_oidhw, DT_F16, 128, 128, 2, 2, A_CONV_GENERIC, B_OIDHW, 4, 1)
-TILE_KERNEL(mtk_conv_f16_gen_128x128_v1_oidhw, DT_F16, 128, 128, 2, 2, A_CONV_GENERIC, B_OIDHW, 1, 1)

@@ -48,8 +48,8 @@ int fail(int status, const char *fmt, ...) {
   } while (0)
 
 constexpr uint64_t kMaxOperandBytes = (1ull << 31) - 256;  // buffer-resource ranges (see device.hpp)
-constexpr int kAutoKStagger = 16;
-constexpr int kMaxHeadDim = MTK_ATTN_MAX_HEAD_DIM;  // largest padded head dimension compiled (256)  // in-workgroup split-K: boundary offsets span up to 16 K-tiles
+constexpr int kAutoKStagger = 16;  // in-workgroup split-K: boundary offsets span up to 16 K-tiles
+constexpr int kMaxHeadDim = MTK_ATTN_MAX_HEAD_DIM;  // largest padded head dimension compiled (256)
 
 }  // namespace
 
@@ -106,6 +106,7 @@ struct mtk_plan {
   mtk_permute_desc perm{};
   std::vector<Launch> launches;
   size_t workspace = 0;
+  size_t weight_bytes = 0;            // conv: exact byte extent of w (its workspace copy is rounded up)
   bool serial_split = false;          // GEMM split-K run in-workgroup (C written by the main kernel)
   unsigned align_a = 2, align_b = 2;  // required operand alignments (bytes)
   double flops = 0, bytes = 0;
@@ -587,10 +588,8 @@ int normalise_conv(const mtk_conv_desc *in, mtk_conv_desc *d) {
   if (d->pad_front < 0 || d->pad_back < 0 || d->pad_top < 0 || d->pad_bottom < 0 || d->pad_left < 0 || d->pad_right < 0)
     return fail(MTK_ERR_INVALID, "padding must be non-negative");
   if (d->dtype != MTK_F16) return fail(MTK_ERR_INVALID, "convolution dtype must be MTK_F16");
-  if (d->weight_layout != MTK_WEIGHTS_DHWIO && d->weight_layout != MTK_WEIGHTS_OIDHW &&
-      d->weight_layout != MTK_WEIGHTS_OIDHW_DIRECT)
-    return fail(MTK_ERR_INVALID,
-                "weight_layout must be MTK_WEIGHTS_DHWIO, MTK_WEIGHTS_OIDHW or MTK_WEIGHTS_OIDHW_DIRECT (got %d)",
+  if (d->weight_layout != MTK_WEIGHTS_DHWIO && d->weight_layout != MTK_WEIGHTS_OIDHW)
+    return fail(MTK_ERR_INVALID, "weight_layout must be MTK_WEIGHTS_DHWIO or MTK_WEIGHTS_OIDHW (got %d)",
                 d->weight_layout);
   int od, oh, ow;
   conv_out(d, &od, &oh, &ow);
@@ -622,10 +621,7 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
   // C % 64 == 0 (every 64-wide K-tile is one filter tap), even O and filter extents <= 10: the
   // direct-to-LDS pipeline (gather with padding as out-of-range loads, weights read transposed).
   // Anything else: the register-staged generic gather.
-  // MTK_WEIGHTS_OIDHW_DIRECT: the register-staged kernel reads the OIDHW weights in place (no
-  // re-layout pass, no workspace; every weight element is a 2-byte load of its own).
-  const bool direct_oidhw = d.weight_layout == MTK_WEIGHTS_OIDHW_DIRECT;
-  const bool fast = !direct_oidhw && (d.C % 64) == 0 && d.O % 2 == 0 && d.KD <= 10 && d.KH <= 10 && d.KW <= 10;
+  const bool fast = (d.C % 64) == 0 && d.O % 2 == 0 && d.KD <= 10 && d.KH <= 10 && d.KW <= 10;
   int va, bm, bn;
   if (fast) {
     va = 8;
@@ -644,11 +640,11 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
     // 140.4 us; 192 tiles 72.4 against 82.5 us).
     if ((M + bm - 1) / bm * ((d.O + bn - 1) / bn) < 140) bm = bn = 128;
   } else {
-    va = direct_oidhw ? pow2_vec({d.C}) : pow2_vec({d.C, d.O});
+    va = pow2_vec({d.C, d.O});
     bm = bn = 128;
   }
   p->align_a = fast ? 16 : 2 * va;
-  p->align_b = fast ? 4 : direct_oidhw ? 2 : 2 * va;
+  p->align_b = fast ? 4 : 2 * va;
   const char *kind = fast ? "fast" : "gen";
   // OIDHW weights (the reference's PermuteThenTensorOpSession3D, ConvolutionShared.swift:1676-1857):
   // the re-layout kernel writes DHWIO weights into the plan's workspace and the convolution reads
@@ -670,12 +666,13 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
     p->align_b = vec ? 16 : 2;
     p->workspace = ((size_t)w_bytes + 255) & ~(size_t)255;
   }
+  p->weight_bytes = (size_t)w_bytes;
   Launch g;
   char name[96];
   if (fast)
     snprintf(name, sizeof name, "mtk_conv_f16_fast_%dx%d_d", bm, bn);
   else
-    snprintf(name, sizeof name, "mtk_conv_f16_gen_%dx%d_v%d%s", bm, bn, va, direct_oidhw ? "_oidhw" : "");
+    snprintf(name, sizeof name, "mtk_conv_f16_gen_%dx%d_v%d", bm, bn, va);
   g.name = name;
   if (fast && bm == 256 && bn == 256) g.block = 512;  // 8 wavefronts
   mtk_tile_args a{};
@@ -722,9 +719,7 @@ int plan_conv(mtk_ctx *ctx, const mtk_conv_desc *d_in, mtk_plan **out) {
   char desc[288];
   snprintf(desc, sizeof desc, "conv%dd f16 implicit-GEMM M=%lld N=%d K=%lld out=%dx%dx%d tile=%dx%d gather=%s grid=%u%s",
            d.rank, M, d.O, K, od, oh, ow, bm, bn, kind, g.grid,
-           oidhw          ? " weights OIDHW (re-laid out in the workspace)"
-           : direct_oidhw ? " weights OIDHW (read in place)"
-                          : "");
+           oidhw ? " weights OIDHW (re-laid out in the workspace)" : "");
   p->description = desc;
   s = resolve(p);
   if (s != MTK_OK) {
@@ -880,7 +875,7 @@ int bind_args(const mtk_plan *p, const void *argset, std::vector<Launch> &ls) {
       return fail(MTK_ERR_INVALID, "this plan needs a 16-byte aligned workspace of %zu bytes", p->workspace);
     if (p->workspace) {
       const char *w0 = (const char *)c->w, *s0 = (const char *)c->workspace;
-      if (w0 < s0 + p->workspace && s0 < w0 + p->workspace) return fail(MTK_ERR_INVALID, "w and workspace overlap");
+      if (w0 < s0 + p->workspace && s0 < w0 + p->weight_bytes) return fail(MTK_ERR_INVALID, "w and workspace overlap");
     }
     for (Launch &l : ls) {
       if (l.role == ROLE_PERMUTE) {

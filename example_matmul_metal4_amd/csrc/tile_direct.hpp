@@ -30,9 +30,6 @@
 
 #include "tile_gemm.hpp"
 
-#ifndef MTK_SLOT_RING
-#define MTK_SLOT_RING 2
-#endif
 
 
 namespace mtk {
@@ -211,13 +208,10 @@ __device__ __forceinline__ void vm_wait() {
 // the two wavefronts of a SIMD belong to different workgroups and drift apart): the one in its
 // MFMA groups issues first, the other's loads and reads fill the gaps. 128x128 convolution 3 %
 // faster; the 256x256 tiles (both wavefronts of a SIMD in one workgroup, in step at its barriers)
-// measured no gain per k-step and 2-3 % slower per MFMA group. MTK_KSTEP_PRIO=0 builds without it.
-#ifndef MTK_KSTEP_PRIO
-#define MTK_KSTEP_PRIO 1
-#endif
+// measured no gain per k-step and 2-3 % slower per MFMA group.
 template <int P>
 __device__ __forceinline__ void mfma_priority() {
-  if constexpr (MTK_KSTEP_PRIO != 0) __builtin_amdgcn_s_setprio(P);
+  __builtin_amdgcn_s_setprio(P);
 }
 
 // Fragments filled by inline-asm LDS reads are handed to their consumers through empty asm
@@ -327,7 +321,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   // other tiles of the XCD are reading (measured: 183 us vs 201 us with sc1 alone at config 2).
   constexpr int kStorePolicy = 16 | 2;
   constexpr int kLoadPolicy = 16 | 2;
-  constexpr int kSlotRing = MTK_SLOT_RING;  // accumulator blocks of the slot in flight
+  constexpr int kSlotRing = 2;  // accumulator blocks of the slot in flight (deeper rings spill)
   const rsrc_t rslot = make_rsrc(SERIAL ? a.partial + (size_t)t * (BM * BN) : nullptr, SERIAL ? kSlotBytes : 0u);
   const uint32_t slot_lane = (uint32_t)(wave * (TM * TN * 1024) + lane * 4) * 4u;
   auto slot_at = [&](int i, int j, int q) { return slot_lane + (uint32_t)((i * TN + j) * 4096 + q * 1024); };
@@ -653,6 +647,9 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     static_assert(NW * WTM * kRowB <= 2 * kStage, "C tile fits the LDS stages");
     // chunk swizzle: the four rows one paired write instruction touches land on disjoint banks
     auto swz = [](int rr) { return kChunks == 16 ? 4 * ((rr & 1) | ((rr >> 1) & 2)) : 4 * ((rr >> 2) & 1); };
+    // The last K-tile's loop reloads a K-tile past the end into the idle stage: those loads must
+    // have landed before the stages hold the C tile (explicit, not left to the fence's own wait).
+    wait_vmem();
     __syncthreads();  // every wave is done reading the last K-tile's fragments
     char *ct = smem + wave * (WTM * kRowB);
     const uint16_t *bias = (const uint16_t *)a.bias;

@@ -32,7 +32,7 @@
 namespace mtk {
 
 enum { A_MK = 0, A_CONV = 1, A_CONV_GENERIC = 2 };
-enum { B_NK = 0, B_KN = 1, B_OIDHW = 2 };
+enum { B_NK = 0, B_KN = 1 };
 
 constexpr int kBK = 64;
 constexpr int kThreads = 256;
@@ -145,46 +145,6 @@ struct LoadColsT {
       if (kBlocks % kThreads != 0 && tid + kThreads * p >= kBlocks) continue;
 #pragma unroll
       for (int j = 0; j < 8; ++j) *(u32x4 *)(lds + lds_off(nb[p] * 8 + j, kb[p])) = in[p * 8 + j];
-    }
-  }
-};
-
-// OIDHW convolution weights read in place as the [K][O] operand of the implicit GEMM (K in the
-// DHWIO order k = tap * C + channel, so the result is the DHWIO convolution's): element (k, o) is
-// w[o][c][t] with t = k / C, c = k % C, at element (o * C + c) * T + t. Consecutive output
-// channels lie C * T elements apart and consecutive channels T apart, so every element is a 2-byte
-// load of its own; the 8x8 blocks are then transposed in registers as in LoadColsT.
-template <int COLS>
-struct LoadOIDHW : LoadColsT<COLS, 1> {
-  using Base = LoadColsT<COLS, 1>;
-  __device__ void load(rsrc_t r, const mtk_tile_args &a, int kt, u32x4 *out, int tid) const {
-    const int C = a.cC;
-    const uint32_t T = (uint32_t)(a.cKD * a.cKH * a.cKW);
-    const uint32_t ostride = (uint32_t)C * T * 2u;  // bytes between output channels
-#pragma unroll
-    for (int p = 0; p < Base::kPer; ++p) {
-      if (Base::kBlocks % kThreads != 0 && tid + kThreads * p >= Base::kBlocks) continue;
-      u32x4 raw[8];
-      const int n = this->n0 + this->nb[p] * 8;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int k = kt * kBK + this->kb[p] * 8 + i;
-        const int t = k / C, c = k - t * C;
-        const uint32_t kofs = ((uint32_t)c * T + (uint32_t)t) * 2u;
-        raw[i] = load_chunk<1>(r, [&](int g) {
-          const int nn = n + g;
-          return (k < a.K && nn < a.N) ? (uint32_t)nn * ostride + kofs : kOOB;
-        });
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int d = j >> 1;
-        uint32_t w[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          w[q] = (j & 1) ? pack_hi(raw[2 * q][d], raw[2 * q + 1][d]) : pack_lo(raw[2 * q][d], raw[2 * q + 1][d]);
-        out[p * 8 + j] = u32x4{w[0], w[1], w[2], w[3]};
-      }
     }
   }
 };
@@ -344,9 +304,7 @@ __device__ __forceinline__ void tile_gemm(const mtk_tile_args &a) {
   constexpr int NA = BM / 32;
   u32x4 rga[NA];
 
-  using LB = typename std::conditional<
-      BKIND == B_NK, LoadRows<BN, VB>,
-      typename std::conditional<BKIND == B_OIDHW, LoadOIDHW<BN>, LoadColsT<BN, VB>>::type>::type;
+  using LB = typename std::conditional<BKIND == B_NK, LoadRows<BN, VB>, LoadColsT<BN, VB>>::type;
   LB lb;
   if constexpr (BKIND == B_NK) {
     lb.init(tid, n0, a.N, a.ldb);
@@ -364,8 +322,6 @@ __device__ __forceinline__ void tile_gemm(const mtk_tile_args &a) {
     }
     if constexpr (BKIND == B_NK) {
       lb.load(rb, kt, a.K, rgb);
-    } else if constexpr (BKIND == B_OIDHW) {
-      lb.load(rb, a, kt, rgb, tid);
     } else {
       lb.load(rb, kt, a.K, a.N, a.ldb, rgb, tid);
     }

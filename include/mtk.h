@@ -249,15 +249,12 @@ int mtk_attn_bwd_run(const mtk_plan *plan, const mtk_attn_bwd_args *args);
  * re-lays the weights out to DHWIO in the caller's workspace (mtk_plan_workspace_bytes, the weight
  * size rounded up to 256 bytes; it must not overlap w), then convolves from there, as the
  * reference's session encodes the permutation and the convolution into one command buffer.
- * weight_layout MTK_WEIGHTS_OIDHW_DIRECT: the same OIDHW weights, read in place by the
- * convolution's weight staging (the permutation fused into the B-operand gather: one kernel, no
- * workspace; the result is bit for bit MTK_WEIGHTS_OIDHW's). Every weight element is then a 2-byte
- * load of its own (neighbouring output channels lie C*KD*KH*KW elements apart), so this runs
- * about 23x slower than MTK_WEIGHTS_OIDHW at the reference's C = O = 512, 3x3x3 profile shape;
- * it is for callers that cannot provide the workspace. */
+ * There is no in-place OIDHW variant: the implicit GEMM's reduction order must be the same for
+ * the activation (channels contiguous per tap) and the weights (taps contiguous per channel in
+ * OIDHW), so one of them has to be transposed, and the one-off re-layout (one read and one write
+ * of the weights per run) is cheaper than a transpose repeated by every output tile. */
 #define MTK_WEIGHTS_DHWIO 0
 #define MTK_WEIGHTS_OIDHW 1
-#define MTK_WEIGHTS_OIDHW_DIRECT 2
 typedef struct {
   int rank; /* 2 or 3 */
   int N, D, H, W, C, O;
@@ -267,8 +264,7 @@ typedef struct {
   int pad_front, pad_back, pad_top, pad_bottom, pad_left, pad_right;
   int has_bias;
   int dtype;         /* MTK_F16 */
-  int weight_layout; /* appended: MTK_WEIGHTS_DHWIO (0, the default), MTK_WEIGHTS_OIDHW or
-                        MTK_WEIGHTS_OIDHW_DIRECT */
+  int weight_layout; /* appended: MTK_WEIGHTS_DHWIO (0, the default) or MTK_WEIGHTS_OIDHW */
 } mtk_conv_desc;
 
 /* Replaces TensorOpSession / TensorOpSession3D / TensorOpBiasSession3D /

@@ -47,7 +47,7 @@ def test_code_objects_hold_every_selectable_kernel():
               "mtk_skinny_f16_long", "mtk_skinny_bf16_long"]
     names += [f"mtk_attn_fwd_{w}{dt}{c}" for w in ("", "pp_") for dt in ("f16", "bf16") for c in ("", "_causal")]
     names += [f"mtk_conv_f16_fast_{t}_d" for t in ("256x256", "128x128")]
-    names += [f"mtk_conv_f16_gen_128x128_v{v}{o}" for v in (8, 4, 1) for o in ("", "_oidhw")]
+    names += [f"mtk_conv_f16_gen_128x128_v{v}" for v in (8, 4, 1)]
     missing = [n for n in names if n.encode() not in blobs]
     assert not missing, missing
 
@@ -243,12 +243,10 @@ def test_conv_kernel_select_and_shapes():
     p = mtk.ConvPlan(None, mtk.conv_desc(d3))
     assert "mtk_conv_f16_fast_128x128_d" in p.describe() and p.out_shape() == (1, 16, 64, 64, 128)
     assert p.work()[0] == d3.flops() == 57982058496
-    # OIDHW weights: re-laid out in the workspace (two kernels), or read in place (one kernel)
+    # OIDHW weights: re-laid out in the workspace, then the same convolution (two kernels)
     p = mtk.ConvPlan(None, mtk.conv_desc(d3, weight_layout="OIDHW"))
     assert p.describe().endswith("kernels: mtk_permute_oidhw_dhwio_v8 mtk_conv_f16_fast_128x128_d")
     assert p.workspace_bytes == 27 * 128 * 128 * 2
-    p = mtk.ConvPlan(None, mtk.conv_desc(d3, weight_layout="OIDHW_DIRECT"))
-    assert p.describe().endswith("kernels: mtk_conv_f16_gen_128x128_v8_oidhw") and p.workspace_bytes == 0
     # the reference's case lists: every output shape agrees with the oracle's formulas
     import json
     cases = json.load(open(os.path.join(ROOT, "tests", "golden", "cases.json")))

@@ -67,6 +67,9 @@ def _check(name, got, exp, bound_terms, dtype):
 
 
 def _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=90, pairs=None, Hkv=None):
+    """GPU forward (for O and lse) and backward once, then the oracle check: on every (b, h) pair,
+    or, with `pairs` (a list of [p0, p1) ranges of flattened b * H + h), on those pairs chunk by
+    chunk (the float64 bound terms cost S_q * S_kv memory per pair)."""
     D = 128
     Hkv = Hkv or H
     group = H // Hkv
@@ -77,7 +80,6 @@ def _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=90, pairs=None, Hkv=N
     G = oracle.normal(seed + 3, (B, Sq, H, D), dtype=dtype)
     O, lse = mtk.attention(dev, Q, K, V, causal=causal, dtype=dtype, return_lse=True)
     dQ, dK, dV = mtk.attention_bwd(dev, Q, K, V, O, G, lse, causal=causal, dtype=dtype)
-    eQ, eK, eV, _ = oracle.attention_bwd(Q, K, V, G, causal=causal, dtype=dtype, pairs=pairs)
     if group > 1:
         # dQ is what full multi-head attention on K/V repeated over each group gives, bit for bit
         Ke, Ve = np.repeat(K, group, 2), np.repeat(V, group, 2)
@@ -85,11 +87,19 @@ def _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=90, pairs=None, Hkv=N
         assert np.array_equal(Oe.view(np.uint16), O.view(np.uint16)) and np.array_equal(lse_e, lse)
         fQ, _, _ = mtk.attention_bwd(dev, Q, Ke, Ve, Oe, G, lse_e, causal=causal, dtype=dtype)
         assert np.array_equal(fQ.view(np.uint16), dQ.view(np.uint16))
-        K, V = Ke, Ve  # magnitudes per query head; the dK/dV terms are summed over the group below
-    sel = slice(None)
-    if pairs is not None:  # compare the computed (b, h) pairs only; Q/K/V magnitudes restricted to them
+    assert all(np.all(np.isfinite(oracle.to_f32(x, dtype))) for x in (dQ, dK, dV))
+    for rng in (pairs or [None]):
+        eQ, eK, eV, _ = oracle.attention_bwd(Q, K, V, G, causal=causal, dtype=dtype, pairs=rng)
+        _check_pairs(Q, K, V, G, dQ, dK, dV, eQ, eK, eV, causal, dtype, group, rng, H)
+
+
+def _check_pairs(Q, K, V, G, dQ, dK, dV, eQ, eK, eV, causal, dtype, group, rng, H):
+    D = Q.shape[3]
+    if group > 1:
+        K, V = np.repeat(K, group, 2), np.repeat(V, group, 2)  # magnitudes per query head
+    if rng is not None:  # compare the computed (b, h) pairs only; Q/K/V magnitudes restricted to them
         assert group == 1
-        bh = [(p // H, p % H) for p in range(*pairs)]
+        bh = [(p // H, p % H) for p in range(*rng)]
         sub = lambda x: np.stack([x[b, :, h] for b, h in bh])[:, :, None]  # [n][S][1][D]
         Q, K, V, G = sub(Q), sub(K), sub(V), sub(G)
         dQ, dK, dV, eQ, eK, eV = (sub(x) for x in (dQ, dK, dV, eQ, eK, eV))
@@ -100,9 +110,9 @@ def _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=90, pairs=None, Hkv=N
     del ads
     back = lambda t: t.transpose(0, 2, 1, 3)  # [B][H][S][D] -> [B][S][H][D]
     per_group = lambda t: t.reshape(t.shape[0], t.shape[1], -1, group, D).sum(3)  # sum a group's query heads
-    _check("dV", dV[sel], eV, per_group(back(p.transpose(0, 1, 3, 2) @ g)), dtype)
-    _check("dK", dK[sel], eK, per_group(back(w.transpose(0, 1, 3, 2) @ q)), dtype)
-    _check("dQ", dQ[sel], eQ, back(w @ k), dtype)
+    _check("dV", dV, eV, per_group(back(p.transpose(0, 1, 3, 2) @ g)), dtype)
+    _check("dK", dK, eK, per_group(back(w.transpose(0, 1, 3, 2) @ q)), dtype)
+    _check("dQ", dQ, eQ, back(w @ k), dtype)
 
 
 @pytest.mark.parametrize("B,H,Sq,Skv,causal,dtype", [
@@ -131,10 +141,10 @@ def test_attention_bwd_grouped_kv_heads(dev, B, H, Hkv, Sq, Skv, causal, dtype):
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_attention_bwd_config5_full_size(dev, causal):
-    # BASELINE config 5 shape (B=2, H=32, S=4096, D=128); every output must be finite, and eight
-    # (b, h) pairs (both batches: b=0 h=28..31, b=1 h=0..3) are checked element by element against
-    # the oracle (which costs ~S^2 D per pair).
-    _run_and_check(dev, 2, 32, 4096, 4096, causal, "f16", seed=10, pairs=(28, 36))
+    # BASELINE config 5 shape (B=2, H=32, S=4096, D=128); every output must be finite, and sixteen
+    # (b, h) pairs in two chunks (b=0 h=0..3 and 28..31, b=1 h=0..3 and 28..31) are checked element
+    # by element against the oracle (which costs ~S^2 D per pair).
+    _run_and_check(dev, 2, 32, 4096, 4096, causal, "f16", seed=10, pairs=[(0, 4), (28, 36), (60, 64)])
 
 
 @pytest.mark.parametrize("q_rows", [128, 256])

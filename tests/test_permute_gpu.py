@@ -51,8 +51,7 @@ def _oidhw(w):
     dict(rank=2, N=1, H=11, W=9, C=3, O=10, PT=1, PB=1, PL=1, PR=1),                   # 2-byte activation loads
 ])
 @pytest.mark.parametrize("bias", [False, True])
-@pytest.mark.parametrize("layout", ["OIDHW", "OIDHW_DIRECT"])
-def test_oidhw_conv_plan(dev, case, bias, layout):
+def test_oidhw_conv_plan(dev, case, bias):
     # the reference's PermuteThenTensorOpSession3D (ConvolutionShared.swift:1676-1857) as one plan:
     # each run re-lays the OIDHW weights out in the workspace and convolves from there; bit-exact
     # against the oracle (integer generators: exact fp32 sums) and against permute-then-conv
@@ -63,8 +62,8 @@ def test_oidhw_conv_plan(dev, case, bias, layout):
     b = gen.conv3d_bias(d) if bias else None
     if rank == 2:
         w = w.reshape(d.KH, d.KW, d.C, d.O)
-    print(f"[oidhw conv] {layout} rank {rank} {case} bias={bias}", flush=True)
-    y = mtk.conv(dev, d, x, _oidhw(w), b, weight_layout=layout)
+    print(f"[oidhw conv] rank {rank} {case} bias={bias}", flush=True)
+    y = mtk.conv(dev, d, x, _oidhw(w), b, weight_layout="OIDHW")
     exp = oracle.conv(d, x, w.reshape(d.w_shape()), b).astype(np.float16).reshape(y.shape)
     assert np.array_equal(y.view(np.uint16), exp.view(np.uint16))
     y2 = mtk.conv(dev, d, x, mtk.permute_oidhw_to_dhwio(dev, _oidhw(w).reshape(d.O, d.C, d.KD, d.KH, d.KW)), b)
@@ -76,10 +75,9 @@ def test_oidhw_conv_plan(dev, case, bias, layout):
     dict(rank=2, N=2, H=13, W=15, C=128, O=256, PT=1, PB=1, PL=1, PR=1),
     dict(rank=3, N=2, D=6, H=7, W=8, C=40, O=36, SZ=2, SX=2, DY=2, PT=2, PB=2),
 ])
-def test_oidhw_direct_random_data(dev, case):
-    # the permutation fused into the weight staging: on seeded U[-1, 1) data (inexact sums) the
-    # in-place OIDHW read gives the re-layout plan's result bit for bit (same K order, same MFMA
-    # operands), which is the DHWIO convolution's
+def test_oidhw_random_data(dev, case):
+    # on seeded U[-1, 1) data (inexact sums) the OIDHW plan gives the DHWIO convolution's result bit
+    # for bit (the re-layout moves bits; the convolution is the same kernel on the same operands)
     case = dict(case)
     rank = case.pop("rank")
     d = (oracle.ConvDims.conv3d if rank == 3 else oracle.ConvDims.conv2d)(**case)
@@ -90,9 +88,8 @@ def test_oidhw_direct_random_data(dev, case):
     wo = np.ascontiguousarray(np.transpose(w, (4, 3, 0, 1, 2)))  # [O][C][KD][KH][KW]
     if rank == 2:
         w, wo = w.reshape(d.KH, d.KW, d.C, d.O), wo.reshape(d.O, d.C, d.KH, d.KW)
-    print(f"[oidhw direct] rank {rank} {case}", flush=True)
-    y = mtk.conv(dev, d, x, wo, b, weight_layout="OIDHW_DIRECT")
-    assert np.array_equal(y.view(np.uint16), mtk.conv(dev, d, x, wo, b, weight_layout="OIDHW").view(np.uint16))
+    print(f"[oidhw random] rank {rank} {case}", flush=True)
+    y = mtk.conv(dev, d, x, wo, b, weight_layout="OIDHW")
     assert np.array_equal(y.view(np.uint16), mtk.conv(dev, d, x, w, b).view(np.uint16))
 
 
@@ -105,8 +102,6 @@ def test_oidhw_conv_reference_profile_shape(dev):
     y = mtk.conv(dev, d, x, _oidhw(w), weight_layout="OIDHW")
     y0 = mtk.conv(dev, d, x, w)
     assert np.array_equal(y.view(np.uint16), y0.view(np.uint16))
-    y1 = mtk.conv(dev, d, x, _oidhw(w), weight_layout="OIDHW_DIRECT")  # permutation fused into the staging
-    assert np.array_equal(y1.view(np.uint16), y0.view(np.uint16))
     rows = y.reshape(-1, d.OW, d.O)
     for r0 in (0, 101, 253):
         exp = oracle.conv(d, x, w, rows=(r0, r0 + 1)).reshape(-1, d.OW, d.O)[r0]
@@ -124,13 +119,29 @@ def test_oidhw_conv_errors(dev):
     with pytest.raises(mtk.MtkError) as e:  # workspace overlapping the weights
         plan.run(x, w, None, y, w.ptr + 256)
     assert "overlap" in e.value.message
-    assert mtk.ConvPlan(dev, mtk.conv_desc(d, weight_layout="OIDHW_DIRECT")).workspace_bytes == 0
-    bad = mtk.conv_desc(d)
-    bad.weight_layout = 7
-    with pytest.raises(mtk.MtkError) as e:
-        mtk.ConvPlan(dev, bad)
-    assert e.value.status == mtk.MTK_ERR_INVALID
+    for layout in (2, 7):  # only DHWIO (0) and OIDHW (1)
+        bad = mtk.conv_desc(d)
+        bad.weight_layout = layout
+        with pytest.raises(mtk.MtkError) as e:
+            mtk.ConvPlan(dev, bad)
+        assert e.value.status == mtk.MTK_ERR_INVALID
     for b in (x, w, y):
+        b.free()
+    # a workspace placed right after weights whose size is not a multiple of 256 bytes does not
+    # overlap them (the workspace is the weight size rounded up; the weights' extent is exact)
+    d = oracle.ConvDims.conv3d(N=1, D=3, H=8, W=8, C=8, O=12)  # 3*3*3*8*12*2 = 5184 bytes
+    plan = mtk.ConvPlan(dev, mtk.conv_desc(d, weight_layout="OIDHW"))
+    wb = 27 * 8 * 12 * 2
+    assert plan.workspace_bytes == (wb + 255) // 256 * 256
+    x, y = dev.empty(3 * 8 * 8 * 8 * 2), dev.empty(6 * 6 * 12 * 2)
+    both = dev.empty(wb + 16 + plan.workspace_bytes)
+    ws = (both.ptr + wb + 15) // 16 * 16
+    plan.run(x, both.ptr, None, y, ws)  # accepted: w ends where the workspace begins
+    with pytest.raises(mtk.MtkError) as e:
+        plan.run(x, both.ptr, None, y, ws - 16)
+    assert "overlap" in e.value.message
+    dev.sync()
+    for b in (x, y, both):
         b.free()
 
 
