@@ -227,6 +227,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (no other configs)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", default="", help="comma-separated prefixes of the other configs' keys to measure "
+                                               "(default: all); the headline always runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the tensor-op path on a single MI355X and has no "
@@ -289,160 +291,176 @@ def main():
     if not args.quick:
         cfgs = {}
         steps = max(10, args.steps // 2)  # the other configs: half the headline's step count
+        only = [o for o in args.only.split(",") if o]
+        want = lambda *keys: not only or any(k.startswith(o) for k in keys for o in only)
         try:
-            p1, s1 = gemm_case(dev, mtk, inputs, M, N, K, "f16", 1, (1, 2, 3),
-                               (nrm(1 / np.sqrt(K)), nrm(1 / np.sqrt(K)), uni(-0.5, 0.5)))
-            tm = time_steps(dev, p1, s1, args.warmup, steps)
-            cfgs["config2_splitk1"] = summarize("config 2 without split-K (split_k=1)", p1, tm, "mfma",
-                                                key="config2_splitk1")
-            p2, s2 = gemm_case(dev, mtk, inputs, M, N, K, "f16", 4, (1, 2, 3),
-                               (nrm(1 / np.sqrt(K)), nrm(1 / np.sqrt(K)), uni(-0.5, 0.5)), split_mode="two_pass")
-            tm = time_steps(dev, p2, s2, args.warmup, steps)
-            cfgs["config2_splitk4_two_pass"] = summarize(
-                "config 2, split-K 4 in the two-pass schedule (partition workgroups + reduce kernel)", p2, tm, "mfma",
-                key="config2_splitk4_two_pass")
-            p3, s3 = gemm_case(dev, mtk, inputs, 16, 14336, 4096, "bf16", 8, (4, 5, 6),
-                               (nrm(1.0), nrm(0.02), nrm(0.02)), copies=3)
-            tm = time_steps(dev, p3, s3, args.warmup, steps * 4)
-            cfgs["config3_decode"] = summarize("config 3: bf16 M=16 N=14336 K=4096 split-K 8 + bias (HBM-bound)",
-                                               p3, tm, "hbm", key="config3_decode")
-            # the reference's own default run (matmul.swift:334): M=32, N=3072, K=80000, split-K 30;
-            # HBM-bound (B is 491 MB), three rotating input copies
-            p4, s4 = gemm_case(dev, mtk, inputs, 32, 3072, 80000, "f16", 30, (50, 51, 52),
-                               (nrm(1 / np.sqrt(80000)), nrm(1 / np.sqrt(80000)), uni(-0.5, 0.5)))
-            tm = time_steps(dev, p4, s4, args.warmup, steps)
-            cfgs["reference_main_large_k"] = summarize("reference main(): f16 M=32 N=3072 K=80000 split-K 30 + bias",
-                                                       p4, tm, "hbm", key="reference_main_large_k")
+            if want("config2_splitk1"):
+                p1, s1 = gemm_case(dev, mtk, inputs, M, N, K, "f16", 1, (1, 2, 3),
+                                   (nrm(1 / np.sqrt(K)), nrm(1 / np.sqrt(K)), uni(-0.5, 0.5)))
+                tm = time_steps(dev, p1, s1, args.warmup, steps)
+                cfgs["config2_splitk1"] = summarize("config 2 without split-K (split_k=1)", p1, tm, "mfma",
+                                                    key="config2_splitk1")
+            if want("config2_splitk4_two_pass"):
+                p2, s2 = gemm_case(dev, mtk, inputs, M, N, K, "f16", 4, (1, 2, 3),
+                                   (nrm(1 / np.sqrt(K)), nrm(1 / np.sqrt(K)), uni(-0.5, 0.5)), split_mode="two_pass")
+                tm = time_steps(dev, p2, s2, args.warmup, steps)
+                cfgs["config2_splitk4_two_pass"] = summarize(
+                    "config 2, split-K 4 in the two-pass schedule (partition workgroups + reduce kernel)", p2, tm, "mfma",
+                    key="config2_splitk4_two_pass")
+            if want("config3_decode"):
+                p3, s3 = gemm_case(dev, mtk, inputs, 16, 14336, 4096, "bf16", 8, (4, 5, 6),
+                                   (nrm(1.0), nrm(0.02), nrm(0.02)), copies=3)
+                tm = time_steps(dev, p3, s3, args.warmup, steps * 4)
+                cfgs["config3_decode"] = summarize("config 3: bf16 M=16 N=14336 K=4096 split-K 8 + bias (HBM-bound)",
+                                                   p3, tm, "hbm", key="config3_decode")
+            if want("reference_main_large_k"):
+                # the reference's own default run (matmul.swift:334): M=32, N=3072, K=80000, split-K 30;
+                # HBM-bound (B is 491 MB), three rotating input copies
+                p4, s4 = gemm_case(dev, mtk, inputs, 32, 3072, 80000, "f16", 30, (50, 51, 52),
+                                   (nrm(1 / np.sqrt(80000)), nrm(1 / np.sqrt(80000)), uni(-0.5, 0.5)))
+                tm = time_steps(dev, p4, s4, args.warmup, steps)
+                cfgs["reference_main_large_k"] = summarize("reference main(): f16 M=32 N=3072 K=80000 split-K 30 + bias",
+                                                           p4, tm, "hbm", key="reference_main_large_k")
             for key, dims in (("config4a_conv2d", dict(rank=2, N=8, D=1, H=128, W=128, C=256, O=256, KD=1, KH=3, KW=3,
-                                                       pad_top=1, pad_bottom=1, pad_left=1, pad_right=1)),
-                              ("config4b_conv3d", dict(rank=3, N=1, D=16, H=64, W=64, C=128, O=128, KD=3, KH=3, KW=3,
-                                                       pad_front=1, pad_back=1, pad_top=1, pad_bottom=1, pad_left=1,
-                                                       pad_right=1))):
-                desc = mtk.ConvDesc(stride_d=1, stride_h=1, stride_w=1, dil_d=1, dil_h=1, dil_w=1, has_bias=1,
-                                    dtype=mtk.F16, **dims)
-                pc = mtk.ConvPlan(dev, desc)
-                shape = pc.out_shape()
-                xs = (desc.N, desc.D, desc.H, desc.W, desc.C)
-                ws_ = (desc.KD, desc.KH, desc.KW, desc.C, desc.O)
-                y = dev.empty(int(np.prod(shape)) * 2)
-                sets_c = [pc.args(dev.upload(inputs.uniform(7 + 100 * c, xs, -1, 1)),
-                                  dev.upload(inputs.uniform(8 + 100 * c, ws_, -1, 1)),
-                                  dev.upload(inputs.uniform(9 + 100 * c, (desc.O,), -1, 1)), y) for c in range(3)]
-                tm = time_steps(dev, pc, sets_c, args.warmup, steps)
-                cfgs[key] = summarize(pc.describe().split(" kernels:")[0], pc, tm, "mfma", key=key)
-            # the reference's published convolution profiles (its only published numbers, M5 iPad
-            # GPU time): conv2d N1 256x256 C=O=512 3x3 at 9.71 TFLOP/s (AGENTS.md:23) and conv3d
-            # N1 D3 256x256 C=O=512 3x3x3 at 9.18 TFLOP/s (AGENTS.md:49-52; largeProfileDimensions,
-            # convolution3d.swift:1316-1334); no padding, stride 1; seeded U[-1,1) data
+                                                           pad_top=1, pad_bottom=1, pad_left=1, pad_right=1)),
+                                  ("config4b_conv3d", dict(rank=3, N=1, D=16, H=64, W=64, C=128, O=128, KD=3, KH=3, KW=3,
+                                                           pad_front=1, pad_back=1, pad_top=1, pad_bottom=1, pad_left=1,
+                                                           pad_right=1))):
+                    if not want(key):
+                        continue
+                    desc = mtk.ConvDesc(stride_d=1, stride_h=1, stride_w=1, dil_d=1, dil_h=1, dil_w=1, has_bias=1,
+                                        dtype=mtk.F16, **dims)
+                    pc = mtk.ConvPlan(dev, desc)
+                    shape = pc.out_shape()
+                    xs = (desc.N, desc.D, desc.H, desc.W, desc.C)
+                    ws_ = (desc.KD, desc.KH, desc.KW, desc.C, desc.O)
+                    y = dev.empty(int(np.prod(shape)) * 2)
+                    sets_c = [pc.args(dev.upload(inputs.uniform(7 + 100 * c, xs, -1, 1)),
+                                      dev.upload(inputs.uniform(8 + 100 * c, ws_, -1, 1)),
+                                      dev.upload(inputs.uniform(9 + 100 * c, (desc.O,), -1, 1)), y) for c in range(3)]
+                    tm = time_steps(dev, pc, sets_c, args.warmup, steps)
+                    cfgs[key] = summarize(pc.describe().split(" kernels:")[0], pc, tm, "mfma", key=key)
+                # the reference's published convolution profiles (its only published numbers, M5 iPad
+                # GPU time): conv2d N1 256x256 C=O=512 3x3 at 9.71 TFLOP/s (AGENTS.md:23) and conv3d
+                # N1 D3 256x256 C=O=512 3x3x3 at 9.18 TFLOP/s (AGENTS.md:49-52; largeProfileDimensions,
+                # convolution3d.swift:1316-1334); no padding, stride 1; seeded U[-1,1) data
             for key, dims, m5 in (("reference_profile_conv2d", dict(rank=2, N=1, D=1, H=256, W=256, C=512, O=512, KD=1,
-                                                                    KH=3, KW=3), 9.71),
-                                  ("reference_profile_conv3d", dict(rank=3, N=1, D=3, H=256, W=256, C=512, O=512, KD=3,
-                                                                    KH=3, KW=3), 9.18)):
-                desc = mtk.ConvDesc(stride_d=1, stride_h=1, stride_w=1, dil_d=1, dil_h=1, dil_w=1, has_bias=0,
-                                    dtype=mtk.F16, **dims)
-                pc = mtk.ConvPlan(dev, desc)
-                shape = pc.out_shape()
-                xs = (desc.N, desc.D, desc.H, desc.W, desc.C)
-                ws_ = (desc.KD, desc.KH, desc.KW, desc.C, desc.O)
-                y = dev.empty(int(np.prod(shape)) * 2)
-                sets_c = [pc.args(dev.upload(inputs.uniform(30 + 100 * c, xs, -1, 1)),
-                                  dev.upload(inputs.uniform(31 + 100 * c, ws_, -1, 1)), None, y) for c in range(3)]
-                tm = time_steps(dev, pc, sets_c, args.warmup, steps)
-                cfgs[key] = summarize(pc.describe().split(" kernels:")[0], pc, tm, "mfma", key=key)
-                cfgs[key]["reference_m5_tflops"] = m5
-                if desc.rank == 3:
-                    # the reference's permute + conv3d session at this shape (AGENTS.md:49-53: 9.07
-                    # TFLOP/s on M5): OIDHW weights re-laid out in the workspace by each run, then the
-                    # same convolution; TFLOP/s counts the convolution's FLOPs only, as there
-                    desc.weight_layout = mtk.WEIGHTS_OIDHW
-                    pf = mtk.ConvPlan(dev, desc)
-                    ws_f = dev.empty(pf.workspace_bytes)
-                    sets_f = [pf.args(sc.x, dev.upload(inputs.uniform(31 + 100 * c, (desc.O, desc.C, desc.KD, desc.KH,
-                                                                                       desc.KW), -1, 1)),
-                                      None, y, ws_f) for c, sc in enumerate(sets_c)]
-                    tm = time_steps(dev, pf, sets_f, args.warmup, steps)
-                    s = summarize(pf.describe().split(" kernels:")[0], pf, tm, "mfma", key="reference_profile_permute_conv3d")
-                    s["reference_m5_tflops"] = 9.07
-                    s["overhead_vs_dhwio_pct"] = 100.0 * (tm[0] / cfgs[key]["ms_per_step"] - 1.0)
-                    cfgs["reference_profile_permute_conv3d"] = s
-            # OIDHW -> DHWIO weight re-layout at the reference's profile shape (512 x 512, 3x3x3;
-            # AGENTS.md:51), HBM-bound: 40 rotating source copies (566 MB with the destination) so the
-            # 256 MB Infinity Cache cannot serve the repeats
-            pp = mtk.PermutePlan(dev, 512, 512, 3, 3, 3)
-            wsh = (512, 512, 3, 3, 3)
-            dst = dev.empty(int(np.prod(wsh)) * 2)
-            wsrc = inputs.normal(14, wsh)
-            sets_p = [pp.args(dev.upload(wsrc), dst) for c in range(40)]
-            tm = time_steps(dev, pp, sets_p, args.warmup, steps * 4)
-            cfgs["conv_weight_permute"] = summarize("OIDHW -> DHWIO weight re-layout, O = C = 512, 3x3x3 (f16)", pp, tm,
-                                                    "hbm", key="conv_weight_permute")
-            cfgs["conv_weight_permute"]["reference_m5_ms"] = 3.42  # AGENTS.md:51
+                                                                        KH=3, KW=3), 9.71),
+                                      ("reference_profile_conv3d", dict(rank=3, N=1, D=3, H=256, W=256, C=512, O=512, KD=3,
+                                                                        KH=3, KW=3), 9.18)):
+                    if not want(key, "reference_profile_permute_conv3d"):
+                        continue
+                    desc = mtk.ConvDesc(stride_d=1, stride_h=1, stride_w=1, dil_d=1, dil_h=1, dil_w=1, has_bias=0,
+                                        dtype=mtk.F16, **dims)
+                    pc = mtk.ConvPlan(dev, desc)
+                    shape = pc.out_shape()
+                    xs = (desc.N, desc.D, desc.H, desc.W, desc.C)
+                    ws_ = (desc.KD, desc.KH, desc.KW, desc.C, desc.O)
+                    y = dev.empty(int(np.prod(shape)) * 2)
+                    sets_c = [pc.args(dev.upload(inputs.uniform(30 + 100 * c, xs, -1, 1)),
+                                      dev.upload(inputs.uniform(31 + 100 * c, ws_, -1, 1)), None, y) for c in range(3)]
+                    tm = time_steps(dev, pc, sets_c, args.warmup, steps)
+                    cfgs[key] = summarize(pc.describe().split(" kernels:")[0], pc, tm, "mfma", key=key)
+                    cfgs[key]["reference_m5_tflops"] = m5
+                    if desc.rank == 3:
+                        # the reference's permute + conv3d session at this shape (AGENTS.md:49-53: 9.07
+                        # TFLOP/s on M5): OIDHW weights re-laid out in the workspace by each run, then the
+                        # same convolution; TFLOP/s counts the convolution's FLOPs only, as there
+                        desc.weight_layout = mtk.WEIGHTS_OIDHW
+                        pf = mtk.ConvPlan(dev, desc)
+                        ws_f = dev.empty(pf.workspace_bytes)
+                        sets_f = [pf.args(sc.x, dev.upload(inputs.uniform(31 + 100 * c, (desc.O, desc.C, desc.KD, desc.KH,
+                                                                                           desc.KW), -1, 1)),
+                                          None, y, ws_f) for c, sc in enumerate(sets_c)]
+                        tm = time_steps(dev, pf, sets_f, args.warmup, steps)
+                        s = summarize(pf.describe().split(" kernels:")[0], pf, tm, "mfma", key="reference_profile_permute_conv3d")
+                        s["reference_m5_tflops"] = 9.07
+                        s["overhead_vs_dhwio_pct"] = 100.0 * (tm[0] / cfgs[key]["ms_per_step"] - 1.0)
+                        cfgs["reference_profile_permute_conv3d"] = s
+            if want("conv_weight_permute"):
+                # OIDHW -> DHWIO weight re-layout at the reference's profile shape (512 x 512, 3x3x3;
+                # AGENTS.md:51), HBM-bound: 40 rotating source copies (566 MB with the destination) so the
+                # 256 MB Infinity Cache cannot serve the repeats
+                pp = mtk.PermutePlan(dev, 512, 512, 3, 3, 3)
+                wsh = (512, 512, 3, 3, 3)
+                dst = dev.empty(int(np.prod(wsh)) * 2)
+                wsrc = inputs.normal(14, wsh)
+                sets_p = [pp.args(dev.upload(wsrc), dst) for c in range(40)]
+                tm = time_steps(dev, pp, sets_p, args.warmup, steps * 4)
+                cfgs["conv_weight_permute"] = summarize("OIDHW -> DHWIO weight re-layout, O = C = 512, 3x3x3 (f16)", pp, tm,
+                                                        "hbm", key="conv_weight_permute")
+                cfgs["conv_weight_permute"]["reference_m5_ms"] = 3.42  # AGENTS.md:51
             for causal in (False, True):
-                pa = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
-                shp = (2, 4096, 32, 128)
-                o = dev.empty(int(np.prod(shp)) * 2)
-                sets_a = [pa.args(dev.upload(inputs.normal(10 + 100 * c, shp)), dev.upload(inputs.normal(11 + 100 * c, shp)),
-                                  dev.upload(inputs.normal(12 + 100 * c, shp)), o) for c in range(2)]
-                tm = time_steps(dev, pa, sets_a, args.warmup, steps)
-                s = summarize(f"config 5: flash-attn fwd B=2 H=32 S=4096 D=128 {'causal' if causal else 'non-causal'}",
-                              pa, tm, "mfma", key="config5_causal" if causal else "config5")
-                s["reference_convention_tflops"] = (2 * 128 + 5) * 4096 * 4096 * 32 * 2 / (
-                    2 if causal else 1) / (tm[0] * 1e-3) / 1e12
-                cfgs["config5_attn_causal" if causal else "config5_attn"] = s
-                # backward of the same shape (the reference's Network.swift gradients): O and lse from
-                # this forward, dO ~ N(0,1); FLOPs = five products of 2 S^2 D per (b, h)
-                pb = mtk.AttentionBwdPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
-                ws_b = dev.empty(pb.workspace_bytes)
-                grads = [dev.empty(int(np.prod(shp)) * 2) for _ in range(3)]
-                sets_b = []
-                for c, sa in enumerate(sets_a):
+                    if not want("config5_attn" + ("_causal" if causal else ""), "config5_attn_bwd" + ("_causal" if causal else "")):
+                        continue
+                    pa = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
+                    shp = (2, 4096, 32, 128)
+                    o = dev.empty(int(np.prod(shp)) * 2)
+                    sets_a = [pa.args(dev.upload(inputs.normal(10 + 100 * c, shp)), dev.upload(inputs.normal(11 + 100 * c, shp)),
+                                      dev.upload(inputs.normal(12 + 100 * c, shp)), o) for c in range(2)]
+                    tm = time_steps(dev, pa, sets_a, args.warmup, steps)
+                    s = summarize(f"config 5: flash-attn fwd B=2 H=32 S=4096 D=128 {'causal' if causal else 'non-causal'}",
+                                  pa, tm, "mfma", key="config5_causal" if causal else "config5")
+                    s["reference_convention_tflops"] = (2 * 128 + 5) * 4096 * 4096 * 32 * 2 / (
+                        2 if causal else 1) / (tm[0] * 1e-3) / 1e12
+                    cfgs["config5_attn_causal" if causal else "config5_attn"] = s
+                    # backward of the same shape (the reference's Network.swift gradients): O and lse from
+                    # this forward, dO ~ N(0,1); FLOPs = five products of 2 S^2 D per (b, h)
+                    pb = mtk.AttentionBwdPlan(dev, 2, 32, 4096, 4096, 128, causal=causal)
+                    ws_b = dev.empty(pb.workspace_bytes)
+                    grads = [dev.empty(int(np.prod(shp)) * 2) for _ in range(3)]
+                    sets_b = []
+                    for c, sa in enumerate(sets_a):
+                        o_c, lse_c = dev.empty(int(np.prod(shp)) * 2), dev.empty(2 * 32 * 4096 * 4)
+                        pa.run(sa.Q, sa.K, sa.V, o_c, lse_c)
+                        sets_b.append(pb.args(sa.Q, sa.K, sa.V, o_c, dev.upload(inputs.normal(13 + 100 * c, shp)), lse_c,
+                                              *grads, ws_b))
+                    dev.sync()
+                    tm = time_steps(dev, pb, sets_b, args.warmup, steps)
+                    cfgs["config5_attn_bwd_causal" if causal else "config5_attn_bwd"] = summarize(
+                        f"config 5 shape, flash-attn backward (dQ, dK, dV) {'causal' if causal else 'non-causal'}", pb, tm,
+                        "mfma", key="config5_bwd_causal" if causal else "config5_bwd")
+            if want("config5_attn_gqa8", "config5_attn_bwd_gqa8"):
+                # grouped K/V heads at the config 5 shape (the reference's Hq / Hk; here Hq = 32, Hk = 8):
+                # forward and backward, non-causal
+                pg = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, H_kv=8)
+                pgb = mtk.AttentionBwdPlan(dev, 2, 32, 4096, 4096, 128, H_kv=8)
+                kvs = (2, 4096, 8, 128)
+                sets_g, sets_gb = [], []
+                ws_g = dev.empty(pgb.workspace_bytes)
+                grads = [dev.empty(int(np.prod(s_)) * 2) for s_ in (shp, kvs, kvs)]
+                for c in range(2):
+                    q_c, k_c, v_c = (dev.upload(inputs.normal(20 + i + 100 * c, s_)) for i, s_ in enumerate((shp, kvs, kvs)))
                     o_c, lse_c = dev.empty(int(np.prod(shp)) * 2), dev.empty(2 * 32 * 4096 * 4)
-                    pa.run(sa.Q, sa.K, sa.V, o_c, lse_c)
-                    sets_b.append(pb.args(sa.Q, sa.K, sa.V, o_c, dev.upload(inputs.normal(13 + 100 * c, shp)), lse_c,
-                                          *grads, ws_b))
+                    sets_g.append(pg.args(q_c, k_c, v_c, o_c, lse_c))
+                    pg.run(q_c, k_c, v_c, o_c, lse_c)
+                    sets_gb.append(pgb.args(q_c, k_c, v_c, o_c, dev.upload(inputs.normal(23 + 100 * c, shp)), lse_c,
+                                            *grads, ws_g))
                 dev.sync()
-                tm = time_steps(dev, pb, sets_b, args.warmup, steps)
-                cfgs["config5_attn_bwd_causal" if causal else "config5_attn_bwd"] = summarize(
-                    f"config 5 shape, flash-attn backward (dQ, dK, dV) {'causal' if causal else 'non-causal'}", pb, tm,
-                    "mfma", key="config5_bwd_causal" if causal else "config5_bwd")
-            # grouped K/V heads at the config 5 shape (the reference's Hq / Hk; here Hq = 32, Hk = 8):
-            # forward and backward, non-causal
-            pg = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, 128, H_kv=8)
-            pgb = mtk.AttentionBwdPlan(dev, 2, 32, 4096, 4096, 128, H_kv=8)
-            kvs = (2, 4096, 8, 128)
-            sets_g, sets_gb = [], []
-            ws_g = dev.empty(pgb.workspace_bytes)
-            grads = [dev.empty(int(np.prod(s_)) * 2) for s_ in (shp, kvs, kvs)]
-            for c in range(2):
-                q_c, k_c, v_c = (dev.upload(inputs.normal(20 + i + 100 * c, s_)) for i, s_ in enumerate((shp, kvs, kvs)))
-                o_c, lse_c = dev.empty(int(np.prod(shp)) * 2), dev.empty(2 * 32 * 4096 * 4)
-                sets_g.append(pg.args(q_c, k_c, v_c, o_c, lse_c))
-                pg.run(q_c, k_c, v_c, o_c, lse_c)
-                sets_gb.append(pgb.args(q_c, k_c, v_c, o_c, dev.upload(inputs.normal(23 + 100 * c, shp)), lse_c,
-                                        *grads, ws_g))
-            dev.sync()
-            tm = time_steps(dev, pg, sets_g, args.warmup, steps)
-            cfgs["config5_attn_gqa8"] = summarize("config 5 shape with 8 K/V heads (H=32, H_kv=8), flash-attn fwd",
-                                                  pg, tm, "mfma", key="config5_gqa8")
-            tm = time_steps(dev, pgb, sets_gb, args.warmup, steps)
-            cfgs["config5_attn_bwd_gqa8"] = summarize(
-                "config 5 shape with 8 K/V heads (H=32, H_kv=8), flash-attn backward", pgb, tm, "mfma",
-                key="config5_bwd_gqa8")
+                tm = time_steps(dev, pg, sets_g, args.warmup, steps)
+                cfgs["config5_attn_gqa8"] = summarize("config 5 shape with 8 K/V heads (H=32, H_kv=8), flash-attn fwd",
+                                                      pg, tm, "mfma", key="config5_gqa8")
+                tm = time_steps(dev, pgb, sets_gb, args.warmup, steps)
+                cfgs["config5_attn_bwd_gqa8"] = summarize(
+                    "config 5 shape with 8 K/V heads (H=32, H_kv=8), flash-attn backward", pgb, tm, "mfma",
+                    key="config5_bwd_gqa8")
             # other head dimensions at the config 5 shape (the reference's run(headDimension:),
             # attention.swift:398): D = 64 and D = 256, both masks
             for hd in (64, 256):
-                shp_d = (2, 4096, 32, hd)
-                o = dev.empty(int(np.prod(shp_d)) * 2)
-                sets_d = [None, None]
-                for c in range(2):
-                    sets_d[c] = (dev.upload(inputs.normal(10 + 100 * c, shp_d)), dev.upload(inputs.normal(11 + 100 * c, shp_d)),
-                                 dev.upload(inputs.normal(12 + 100 * c, shp_d)))
-                for causal in (False, True):
-                    pd = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, hd, causal=causal)
-                    tm = time_steps(dev, pd, [pd.args(*t_, o) for t_ in sets_d], args.warmup, steps)
-                    key = f"config5_attn_d{hd}" + ("_causal" if causal else "")
-                    cfgs[key] = summarize(f"config 5 shape, head dimension {hd}, flash-attn fwd "
-                                          f"{'causal' if causal else 'non-causal'}", pd, tm, "mfma", key=key)
+                    if not want(f"config5_attn_d{hd}"):
+                        continue
+                    shp_d = (2, 4096, 32, hd)
+                    o = dev.empty(int(np.prod(shp_d)) * 2)
+                    sets_d = [None, None]
+                    for c in range(2):
+                        sets_d[c] = (dev.upload(inputs.normal(10 + 100 * c, shp_d)), dev.upload(inputs.normal(11 + 100 * c, shp_d)),
+                                     dev.upload(inputs.normal(12 + 100 * c, shp_d)))
+                    for causal in (False, True):
+                        pd = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, hd, causal=causal)
+                        tm = time_steps(dev, pd, [pd.args(*t_, o) for t_ in sets_d], args.warmup, steps)
+                        key = f"config5_attn_d{hd}" + ("_causal" if causal else "")
+                        cfgs[key] = summarize(f"config 5 shape, head dimension {hd}, flash-attn fwd "
+                                              f"{'causal' if causal else 'non-causal'}", pd, tm, "mfma", key=key)
         except Exception as e:  # report what was measured; the headline stands on its own
             cfgs["error"] = repr(e)
         line["configs"] = cfgs

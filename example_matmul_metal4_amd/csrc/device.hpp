@@ -133,6 +133,12 @@ __device__ __forceinline__ void lds_direct16(rsrc_t r, char *lds, uint32_t off) 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, off, 0, 0, 0);
 }
 
+// This lane's index in its wavefront, computed afresh (mbcnt), not derived from threadIdx: code
+// after a long loop that takes it from here holds nothing lane-specific across the loop.
+__device__ __forceinline__ int lane_id() {
+  return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
 // Wait until every vector-memory load of this wave has completed, direct-to-LDS ones included.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 

@@ -323,10 +323,18 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   constexpr int kLoadPolicy = 16 | 2;
   constexpr int kSlotRing = 2;  // accumulator blocks of the slot in flight (deeper rings spill)
   const rsrc_t rslot = make_rsrc(SERIAL ? a.partial + (size_t)t * (BM * BN) : nullptr, SERIAL ? kSlotBytes : 0u);
-  const uint32_t slot_lane = (uint32_t)(wave * (TM * TN * 1024) + lane * 4) * 4u;
-  auto slot_at = [&](int i, int j, int q) { return slot_lane + (uint32_t)((i * TN + j) * 4096 + q * 1024); };
-  auto slot_load = [&](int i, int j, int q) {
-    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rslot, slot_at(i, j, q), 0, kLoadPolicy));
+  // this lane's first slot byte (recomputed where used, so it is not held across the K loop)
+  auto slot_lane_at = [&]() {
+    int l = lane_id();
+    asm volatile("" : "+v"(l));
+    return (uint32_t)(wave * (TM * TN * 1024) + l * 4) * 4u;
+  };
+  // The block's byte offset within the wave's part of the slot goes in the scalar offset operand
+  // (it exceeds the 12-bit immediate): the lane part stays one register. Per-block lane offsets
+  // were otherwise held in 32 registers across the K loop, and spilled.
+  auto slot_blk = [](int i, int j, int q) { return (i * TN + j) * 4096 + q * 1024; };
+  auto slot_load = [&](uint32_t slot_lane, int i, int j, int q) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rslot, slot_lane, slot_blk(i, j, q), kLoadPolicy));
   };
   int split_end = SERIAL ? split_first_tile(a, 1, t) : 0;  // SERIAL: first K-tile of the next partition
   int parked = 0;                                           // SERIAL: partitions parked in the workspace
@@ -452,6 +460,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
         pre = true;
         frag_wait<0>(fa[0], fb[0]);
         frag_tie(fa[1], fb[1]);
+        const uint32_t slot_lane = slot_lane_at();
         if (parked == 0) {
   #pragma unroll
           for (int i = 0; i < TM; ++i)
@@ -462,7 +471,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
                 __builtin_amdgcn_raw_buffer_store_b128(
                     __builtin_bit_cast(u32x4, f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                                                     acc[i][j][4 * q + 3]}),
-                    rslot, slot_at(i, j, q), 0, kStorePolicy);
+                    rslot, slot_lane, slot_blk(i, j, q), kStorePolicy);
         } else {
           // slot += partition sum, one accumulator block at a time, the next kSlotRing-1 blocks'
           // loads in flight
@@ -470,20 +479,20 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   #pragma unroll
           for (int b = 0; b + 1 < kSlotRing; ++b)
   #pragma unroll
-            for (int q = 0; q < 4; ++q) ring[b][q] = slot_load(b % TM, b / TM, q);
+            for (int q = 0; q < 4; ++q) ring[b][q] = slot_load(slot_lane, b % TM, b / TM, q);
   #pragma unroll
           for (int b = 0; b < TM * TN; ++b) {
             const int i = b % TM, j = b / TM;
             constexpr int kAhead = kSlotRing - 1;
             if (b + kAhead < TM * TN) {
   #pragma unroll
-              for (int q = 0; q < 4; ++q) ring[(b + kAhead) % kSlotRing][q] = slot_load((b + kAhead) % TM, (b + kAhead) / TM, q);
+              for (int q = 0; q < 4; ++q) ring[(b + kAhead) % kSlotRing][q] = slot_load(slot_lane, (b + kAhead) % TM, (b + kAhead) / TM, q);
             }
   #pragma unroll
             for (int q = 0; q < 4; ++q) {
               const f32x4 v = ring[b % kSlotRing][q] +
                               f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rslot, slot_at(i, j, q), 0,
+              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rslot, slot_lane, slot_blk(i, j, q),
                                                      kStorePolicy);
             }
           }
@@ -532,11 +541,20 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     // out in the first MFMA groups of K-tile kt and are waited for at one barrier before its last
     // k-step. (The two-ahead ring measured 2-5 % slower on this gather, whose loads of K-tile kt + 2
     // then come in the second half of K-tile kt; on the 128x128 convolution it is 1-2 % faster.)
+    // K-tiles are visited channel-block-major: all filter taps of channels 0..63, then of 64..127,
+    // and so on (K-tile kt of the visit is tap kt % T of channel block kt / T, i.e. K-tile
+    // (kt % T) * (C / 64) + kt / T of the tap-major K order the operands are laid out in). The
+    // gather's reuse distance is shorter than tap-major (neighbouring taps read overlapping pixel
+    // windows one after the other): conv2d 177.9 -> 172.1 us, the reference's 512-channel conv2d
+    // profile shape 336.8 -> 324.8 us. (With 128 channels, as at config 4b's 128x128 tiles, tap-major
+    // measured faster: both halves of a pixel's 256-byte channel row are then read back to back.)
     static_assert(!SERIAL && !kAnyTail, "convolutions never split K and have whole K-tiles");
+    const int taps = a.cKD * a.cKH * a.cKW, cblocks = a.cC / kBK;
+    auto kmap = [&](int kt) { return (kt % taps) * cblocks + kt / taps; };
     constexpr int kGroups1 = (kBK / 16) * TM;
     constexpr int kLoadGroups1 = 8 < kGroups1 - TM ? 8 : kGroups1 - TM;
     constexpr int kPerGroup1 = (PA + PB + kLoadGroups1 - 1) / kLoadGroups1;
-    if (kt0 < kt1) issue_all(smem, kt0);
+    if (kt0 < kt1) issue_all(smem, kmap(kt0));
     wait_vmem();
     __syncthreads();
     u32x4 ga[2][TM], gb[2][TN];
@@ -548,7 +566,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       const int cur = (kt - kt0) & 1;
       char *nxt = smem + (cur ^ 1) * kStage;
       // the last iteration reloads the current K-tile into the idle stage (L2 hits, never computed)
-      const int kn = min(kt + 1, kt1 - 1);
+      const int kn = kmap(min(kt + 1, kt1 - 1));
       const char *sa = smem + cur * kStage;
       const char *sb = sa + BM * 128;
       const auto tp = opa.tap(a, kn);
@@ -599,9 +617,13 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   // column l%32 of its block. Adjacent lanes swap one value of each register pair (DPP quad_perm
   // [1,0,3,2]) so every lane then holds two adjacent columns of one row: even lanes row R, odd
   // lanes row R+1. Half the store instructions, each 4 bytes (f16/bf16) or 8 bytes (fp32 partial).
-  const bool odd = lane & 1;
-  const int col_l = (lane & 31) & ~1;
-  const int row_l = 4 * (lane >> 5) + (odd ? 1 : 0);
+  // The epilogue takes the lane index afresh: nothing it derives from it (columns, bias values,
+  // LDS addresses) is computed before the K loop and held, or spilled, across it.
+  int lane_e = lane_id();
+  asm volatile("" : "+v"(lane_e));
+  const bool odd = lane_e & 1;
+  const int col_l = (lane_e & 31) & ~1;
+  const int row_l = 4 * (lane_e >> 5) + (odd ? 1 : 0);
   const int mw = m0 + wave_m * WTM + row_l, nw = n0 + wave_n * WTN + col_l;
   auto pair = [&](float x0, float x1, float &lo, float &hi) {
     const float send = odd ? x0 : x1;
@@ -656,11 +678,12 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     // SERIAL: the running sum of the earlier partitions, loaded one accumulator block ahead and
     // added in front of the last partition's sum.
     const bool has_slot = SERIAL && parked > 0;
+    const uint32_t slot_lane = SERIAL ? slot_lane_at() : 0u;
     f32x4 ring[kSlotRing][4];
     auto fetch = [&](int s, int i, int j) {
       if (has_slot) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ring[s][q] = slot_load(i, j, q);
+        for (int q = 0; q < 4; ++q) ring[s][q] = slot_load(slot_lane, i, j, q);
       }
     };
     if constexpr (SERIAL) {
@@ -706,7 +729,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     constexpr int kRowsPerInst = 64 / kChunks;
 #pragma unroll 4
     for (int it = 0; it < WTM / kRowsPerInst; ++it) {
-      const int rr = it * kRowsPerInst + lane / kChunks, ch = lane % kChunks;
+      const int rr = it * kRowsPerInst + lane_e / kChunks, ch = lane_e % kChunks;
       const u32x4 v = *(const u32x4 *)(ct + rr * kRowB + ((ch ^ swz(rr)) << 4));
       const int grow = gr0 + rr, gcol = gc0 + 8 * ch;
       if (grow < a.M) {
