@@ -447,20 +447,36 @@ def main():
             # other head dimensions at the config 5 shape (the reference's run(headDimension:),
             # attention.swift:398): D = 64 and D = 256, both masks
             for hd in (64, 256):
-                    if not want(f"config5_attn_d{hd}"):
-                        continue
-                    shp_d = (2, 4096, 32, hd)
-                    o = dev.empty(int(np.prod(shp_d)) * 2)
-                    sets_d = [None, None]
-                    for c in range(2):
-                        sets_d[c] = (dev.upload(inputs.normal(10 + 100 * c, shp_d)), dev.upload(inputs.normal(11 + 100 * c, shp_d)),
-                                     dev.upload(inputs.normal(12 + 100 * c, shp_d)))
-                    for causal in (False, True):
-                        pd = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, hd, causal=causal)
-                        tm = time_steps(dev, pd, [pd.args(*t_, o) for t_ in sets_d], args.warmup, steps)
-                        key = f"config5_attn_d{hd}" + ("_causal" if causal else "")
-                        cfgs[key] = summarize(f"config 5 shape, head dimension {hd}, flash-attn fwd "
-                                              f"{'causal' if causal else 'non-causal'}", pd, tm, "mfma", key=key)
+                if not want(f"config5_attn_d{hd}"):
+                    continue
+                shp_d = (2, 4096, 32, hd)
+                o = dev.empty(int(np.prod(shp_d)) * 2)
+                sets_d = [None, None]
+                for c in range(2):
+                    sets_d[c] = (dev.upload(inputs.normal(10 + 100 * c, shp_d)), dev.upload(inputs.normal(11 + 100 * c, shp_d)),
+                                 dev.upload(inputs.normal(12 + 100 * c, shp_d)))
+                for causal in (False, True):
+                    pd = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, hd, causal=causal)
+                    tm = time_steps(dev, pd, [pd.args(*t_, o) for t_ in sets_d], args.warmup, steps)
+                    key = f"config5_attn_d{hd}" + ("_causal" if causal else "")
+                    cfgs[key] = summarize(f"config 5 shape, head dimension {hd}, flash-attn fwd "
+                                          f"{'causal' if causal else 'non-causal'}", pd, tm, "mfma", key=key)
+                # the backward at this head dimension (non-causal): O and lse from the forward
+                pdf = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, hd)
+                pdb = mtk.AttentionBwdPlan(dev, 2, 32, 4096, 4096, hd)
+                ws_db = dev.empty(pdb.workspace_bytes)
+                grads = [dev.empty(int(np.prod(shp_d)) * 2) for _ in range(3)]
+                sets_db = []
+                for c, t_ in enumerate(sets_d):
+                    o_c, lse_c = dev.empty(int(np.prod(shp_d)) * 2), dev.empty(2 * 32 * 4096 * 4)
+                    pdf.run(*t_, o_c, lse_c)
+                    sets_db.append(pdb.args(*t_, o_c, dev.upload(inputs.normal(13 + 100 * c, shp_d)), lse_c, *grads,
+                                            ws_db))
+                dev.sync()
+                tm = time_steps(dev, pdb, sets_db, args.warmup, steps)
+                key = f"config5_attn_bwd_d{hd}"
+                cfgs[key] = summarize(f"config 5 shape, head dimension {hd}, flash-attn backward (dQ, dK, dV) "
+                                      "non-causal", pdb, tm, "mfma", key=key)
         except Exception as e:  # report what was measured; the headline stands on its own
             cfgs["error"] = repr(e)
         line["configs"] = cfgs

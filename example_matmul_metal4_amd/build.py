@@ -24,7 +24,8 @@ CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-HIP_UNITS = ["gemm_f16", "gemm_bf16", "conv", "attention", "attention_hd", "attention_bwd", "skinny", "permute", "util"]
+HIP_UNITS = ["gemm_f16", "gemm_bf16", "conv", "attention", "attention_hd", "attention_bwd", "attention_bwd256", "skinny",
+             "permute", "util"]
 
 HIPCC_FLAGS = [
     "--genco", "--offload-arch=gfx950", "-O3", "-std=c++17",

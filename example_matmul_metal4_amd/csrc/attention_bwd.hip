@@ -1,4 +1,6 @@
-// Flash-attention backward for gfx950 (head dim 128), fp16/bf16 in and out, fp32 accumulate.
+// Flash-attention backward for gfx950 (head dimensions that are multiples of 8 up to 128: the
+// kernels are laid out for 128, chunks of 8 elements past D are loaded as zeros, contribute exact
+// zeros to every product, and are not stored), fp16/bf16 in and out, fp32 accumulate.
 //
 // The reference has no GPU backward; its CPU restatement of the gradients of the loss
 // Phi = sum dO * O is Sources/attention/Network.swift:205-281 (dP row, D-term, dS row) and
@@ -31,7 +33,7 @@
 
 namespace mtk {
 
-constexpr int kBD = 128;                 // head dimension
+constexpr int kBD = 128;                 // padded head dimension
 constexpr int kRowTile = 64 * kBD * 2;   // one 64-row operand tile in LDS: 16 KB
 constexpr int kBwdKeys = 128;            // keys per dK/dV workgroup
 constexpr int kBwdQTile = 64;            // queries per LDS tile of the dK/dV kernel
@@ -82,16 +84,18 @@ __device__ __forceinline__ void lgkm_wait_n(u32x4 &f) {
 
 // Stage rows [row0, row0 + 4 * n) of a 64-row operand tile: instruction i fills 4 rows (1 KB),
 // lane l writes row row0 + 4 i + l / 16, LDS chunk l % 16, which holds global chunk
-// (l % 16) ^ swizzle(row). Rows at or past `rows_valid` read zero.
+// (l % 16) ^ swizzle(row). Rows at or past `rows_valid` and chunks at or past `nchunk` (head
+// dimensions below 128: 8 elements per chunk) read zero.
 template <int N, bool TR>
 __device__ __forceinline__ void stage_rows(rsrc_t r, char *tile, int row0, uint32_t base, uint32_t rs, int rows_valid,
-                                           int lane) {
+                                           int nchunk, int lane) {
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const int row = row0 + 4 * i + (lane >> 4);
     const int pc = lane & 15;
     const int gc = TR ? (pc ^ (4 * (row & 3))) : (pc ^ (row & 15));
-    lds_direct16(r, tile + (row0 + 4 * i) * 256, row < rows_valid ? base + (uint32_t)row * rs + 16u * gc : kOOB);
+    lds_direct16(r, tile + (row0 + 4 * i) * 256,
+                 row < rows_valid && gc < nchunk ? base + (uint32_t)row * rs + 16u * gc : kOOB);
   }
 }
 
@@ -99,20 +103,23 @@ __device__ __forceinline__ void stage_rows(rsrc_t r, char *tile, int row0, uint3
 
 template <int DT>
 __device__ __forceinline__ void attn_bwd_pre(const mtk_attn_bwd_kargs &a) {
-  // 16 lanes per (b, q, h) row of 128: lane loads 8 elements of O and dO
+  // 16 lanes per (b, q, h) row of D <= 256 elements: lane j takes elements 8 j .. 8 j + 7 of O and
+  // dO, then (D > 128) 8 (j + 16) .. + 7 (zero past D)
   const long long row = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
   const long long rows = (long long)a.B * a.S_q * a.H;
   if (row >= rows) return;
   const int j = threadIdx.x & 15;
   const rsrc_t ro = make_rsrc(a.O, a.q_bytes);
   const rsrc_t rg = make_rsrc(a.dO, a.q_bytes);
-  const uint32_t off = (uint32_t)(row * kBD + 8 * j) * 2u;
-  const u32x4 o = buf_load16(ro, off), g = buf_load16(rg, off);
   float s = 0.0f;
+  for (int cj = j; cj < 32 && 8 * (cj - j) < a.D; cj += 16) {
+    const uint32_t off = 8 * cj < a.D ? (uint32_t)(row * a.D + 8 * cj) * 2u : kOOB;
+    const u32x4 o = buf_load16(ro, off), g = buf_load16(rg, off);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    s = __builtin_fmaf(from_bits<DT>(o[e] & 0xffffu), from_bits<DT>(g[e] & 0xffffu), s);
-    s = __builtin_fmaf(from_bits<DT>(o[e] >> 16), from_bits<DT>(g[e] >> 16), s);
+    for (int e = 0; e < 4; ++e) {
+      s = __builtin_fmaf(from_bits<DT>(o[e] & 0xffffu), from_bits<DT>(g[e] & 0xffffu), s);
+      s = __builtin_fmaf(from_bits<DT>(o[e] >> 16), from_bits<DT>(g[e] >> 16), s);
+    }
   }
 #pragma unroll
   for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m, 16);
@@ -151,8 +158,10 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   const int b = bh / a.H_kv, hk = bh - b * a.H_kv;
   const int group = a.H / a.H_kv;  // query heads hk * group .. hk * group + group - 1
   const int k0 = kb * kBwdKeys;
-  const uint32_t rs = (uint32_t)a.H * kBD * 2, rkv = (uint32_t)a.H_kv * kBD * 2;
-  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H_kv + hk) * kBD * 2);
+  // rows of D elements (a multiple of 8, at most 128): chunks at or past nchunk are zeros
+  const int nchunk = a.D >> 3;
+  const uint32_t rs = (uint32_t)a.H * a.D * 2, rkv = (uint32_t)a.H_kv * a.D * 2;
+  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H_kv + hk) * a.D * 2);
   const rsrc_t rq = make_rsrc(a.Q, a.q_bytes);
   const rsrc_t rg = make_rsrc(a.dO, a.q_bytes);
   const rsrc_t rk = make_rsrc(a.K, a.kv_bytes);
@@ -169,7 +178,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   u32x4 kf[8], vf[8];
 #pragma unroll
   for (int ds = 0; ds < 8; ++ds) {
-    const uint32_t off = key_ok ? kvbase + (uint32_t)key * rkv + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB;
+    const uint32_t off = key_ok && 2 * ds + g < nchunk ? kvbase + (uint32_t)key * rkv + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB;
     kf[ds] = buf_load16(rk, off);
     vf[ds] = buf_load16(rv, off);
   }
@@ -189,7 +198,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     const int h = hk * group + i / per_head;
     t = t0 + i % per_head;
     valid = a.S_q - t * kBwdQTile;
-    const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kBD * 2);
+    const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * a.D * 2);
     row_base = (uint32_t)(((size_t)b * a.H + h) * a.S_q) * 4u;
     tb = qbase + (uint32_t)(t * kBwdQTile) * rs;
   };
@@ -198,16 +207,16 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     int valid, t;
     uint32_t tb, row_base;
     tile_of(i, valid, tb, row_base, t);
-    stage_rows<4, false>(rq, st, 16 * wave, tb, rs, valid, lane);
-    stage_rows<4, false>(rg, st + kRowTile, 16 * wave, tb, rs, valid, lane);
+    stage_rows<4, false>(rq, st, 16 * wave, tb, rs, valid, nchunk, lane);
+    stage_rows<4, false>(rg, st + kRowTile, 16 * wave, tb, rs, valid, nchunk, lane);
   };
   auto stage_tr_to = [&](int slot, int i) {
     char *st = smem + kTrOff + slot * kPair;
     int valid, t;
     uint32_t tb, row_base;
     tile_of(i, valid, tb, row_base, t);
-    stage_rows<4, true>(rq, st, 16 * wave, tb, rs, valid, lane);
-    stage_rows<4, true>(rg, st + kRowTile, 16 * wave, tb, rs, valid, lane);
+    stage_rows<4, true>(rq, st, 16 * wave, tb, rs, valid, nchunk, lane);
+    stage_rows<4, true>(rg, st + kRowTile, 16 * wave, tb, rs, valid, nchunk, lane);
     // lse (wave 0) and D (wave 1) of the tile's queries: lanes 0-15 load 4 values each (entries past
     // S_q are never used unmasked); lanes 16-63 write zeros
     if (wave < 2) {
@@ -393,15 +402,15 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   __syncthreads();
   uint16_t *dK = (uint16_t *)a.dK;
   uint16_t *dV = (uint16_t *)a.dV;
-  const size_t base0 = ((size_t)b * a.S_kv * a.H_kv + hk) * kBD;
+  const size_t base0 = ((size_t)b * a.S_kv * a.H_kv + hk) * a.D;
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
     const int r = 4 * it + (lane >> 4), pc = lane & 15;
     const int kr = k0 + wave * 32 + r;
     const uint32_t o = (uint32_t)(r * 256 + ((pc ^ (r & 15)) << 4));
     const u32x4 vk = *(const u32x4 *)(pk + o), vv = *(const u32x4 *)(pv + o);
-    if (kr < a.S_kv) {
-      const size_t e = base0 + (size_t)kr * a.H_kv * kBD + 8 * pc;
+    if (kr < a.S_kv && pc < nchunk) {
+      const size_t e = base0 + (size_t)kr * a.H_kv * a.D + 8 * pc;
       *(u32x4 *)(dK + e) = vk;
       *(u32x4 *)(dV + e) = vv;
     }
@@ -429,9 +438,10 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
   const int b = bh / a.H, h = bh - b * a.H;
   const int hk = h / (a.H / a.H_kv);  // K/V head of query head h
   const int q0 = qblk * kBwdQRows;
-  const uint32_t rs = (uint32_t)a.H * kBD * 2, rkv = (uint32_t)a.H_kv * kBD * 2;
-  const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * kBD * 2);
-  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H_kv + hk) * kBD * 2);
+  const int nchunk = a.D >> 3;  // rows of D elements: chunks at or past nchunk are zeros
+  const uint32_t rs = (uint32_t)a.H * a.D * 2, rkv = (uint32_t)a.H_kv * a.D * 2;
+  const uint32_t qbase = (uint32_t)(((size_t)b * a.S_q * a.H + h) * a.D * 2);
+  const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H_kv + hk) * a.D * 2);
   const rsrc_t rq = make_rsrc(a.Q, a.q_bytes);
   const rsrc_t rg = make_rsrc(a.dO, a.q_bytes);
   const rsrc_t rk = make_rsrc(a.K, a.kv_bytes);
@@ -445,7 +455,7 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
   u32x4 qf[8], gf[8];
 #pragma unroll
   for (int ds = 0; ds < 8; ++ds) {
-    const uint32_t off = q_ok ? qbase + (uint32_t)qi * rs + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB;
+    const uint32_t off = q_ok && 2 * ds + g < nchunk ? qbase + (uint32_t)qi * rs + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB;
     qf[ds] = buf_load16(rq, off);
     gf[ds] = buf_load16(rg, off);
   }
@@ -461,9 +471,9 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
     char *st = smem + slot * 3 * kRowTile;
     const int valid = a.S_kv - t * kBwdKTile;
     const uint32_t tb = kvbase + (uint32_t)(t * kBwdKTile) * rkv;
-    stage_rows<2, false>(rk, st, 8 * wave, tb, rkv, valid, lane);
-    stage_rows<2, true>(rk, st + kRowTile, 8 * wave, tb, rkv, valid, lane);
-    stage_rows<2, false>(rv, st + 2 * kRowTile, 8 * wave, tb, rkv, valid, lane);
+    stage_rows<2, false>(rk, st, 8 * wave, tb, rkv, valid, nchunk, lane);
+    stage_rows<2, true>(rk, st + kRowTile, 8 * wave, tb, rkv, valid, nchunk, lane);
+    stage_rows<2, false>(rv, st + 2 * kRowTile, 8 * wave, tb, rkv, valid, nchunk, lane);
   };
 
   const int arow = bwd_swap_bits_2_3(col);  // MFMA row m reads key swap_bits_2_3(m) of the block
@@ -584,7 +594,7 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
     const int r = 4 * it + (lane >> 4), pc = lane & 15;
     const int qr = q0 + wave * 32 + r;
     const u32x4 v = *(const u32x4 *)(pq + r * 256 + ((pc ^ (r & 15)) << 4));
-    if (qr < a.S_q) *(u32x4 *)(dQ + (((size_t)b * a.S_q + qr) * a.H + h) * kBD + 8 * pc) = v;
+    if (qr < a.S_q && pc < nchunk) *(u32x4 *)(dQ + (((size_t)b * a.S_q + qr) * a.H + h) * a.D + 8 * pc) = v;
   }
 }
 

@@ -9,7 +9,7 @@
 
 #include <stdint.h>
 
-#define MTK_KARGS_VERSION 9
+#define MTK_KARGS_VERSION 10
 
 /* Tile-GEMM kernels: plain GEMM (A [M][K] . B, B either [N][K] or [K][N]) and
  * implicit-GEMM convolution (A = im2col of an NDHWC activation, B = DHWIO
@@ -109,6 +109,7 @@ typedef struct {
   float scale;      /* 1 / sqrt(D) */
   uint32_t q_bytes, kv_bytes;
   float *Lt; /* [B][H][S_q] workspace: lse * log2(e) (base-2 log-sum-exp) */
+  int32_t D; /* head dimension: a multiple of 8 up to the kernel's padded head dimension */
 } mtk_attn_bwd_kargs;
 
 /* Convolution weight re-layout OIDHW -> DHWIO (16-bit elements). */

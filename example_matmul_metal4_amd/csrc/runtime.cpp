@@ -451,7 +451,11 @@ int plan_attn_bwd(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   if (d.H_kv == 0) d.H_kv = d.H;
   if (d.H_kv < 0 || d.H % d.H_kv != 0)
     return fail(MTK_ERR_INVALID, "H_kv must divide H (got H=%d, H_kv=%d)", d.H, d.H_kv);
-  if (d.D != 128) return fail(MTK_ERR_UNSUPPORTED, "head dimension must be 128 (got %d)", d.D);
+  if (d.D <= 0 || d.D > 256 || d.D % 8 != 0)
+    return fail(MTK_ERR_UNSUPPORTED, "backward head dimension must be a multiple of 8 up to 256 (got %d)", d.D);
+  // D <= 128: the 32-key / 32-query wavefront kernels laid out for 128 (chunks past D are zeros);
+  // 128 < D <= 256: the 16-key / 16-query wavefront kernels laid out for 256
+  const bool wide = d.D > 128;
   if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "attention dtype must be MTK_F16 or MTK_BF16");
   if (d.q_rows != 0) return fail(MTK_ERR_INVALID, "the backward plan chooses its own blocking (q_rows must be 0)");
   const uint64_t q_bytes = (uint64_t)d.B * d.S_q * d.H * d.D * 2;
@@ -471,21 +475,22 @@ int plan_attn_bwd(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   a.H_kv = d.H_kv;
   a.S_q = d.S_q;
   a.S_kv = d.S_kv;
-  a.q_blocks = (d.S_q + 255) / 256;
-  a.k_blocks = (d.S_kv + 127) / 128;
+  a.q_blocks = wide ? (d.S_q + 63) / 64 : (d.S_q + 255) / 256;
+  a.k_blocks = wide ? (d.S_kv + 63) / 64 : (d.S_kv + 127) / 128;
   a.causal = d.causal ? 1 : 0;
   a.scale = (float)(1.0 / std::sqrt((double)d.D));
   a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)d.D));
   a.q_bytes = (uint32_t)q_bytes;
   a.kv_bytes = (uint32_t)kv_bytes;
+  a.D = d.D;
   Launch pre, kv, q;
   pre.name = std::string("mtk_attn_bwd_pre_") + dt;
   pre.grid = (unsigned)(((long long)d.B * d.S_q * d.H + 15) / 16);
-  kv.name = std::string("mtk_attn_bwd_dkdv_") + dt + cz;
+  kv.name = std::string(wide ? "mtk_attn_bwd256_dkdv_" : "mtk_attn_bwd_dkdv_") + dt + cz;
   kv.grid = (unsigned)((long long)a.k_blocks * d.B * d.H_kv);  // per K/V head: sums over its query heads
-  q.name = std::string("mtk_attn_bwd_dq_") + dt + cz;
+  q.name = std::string(wide ? "mtk_attn_bwd256_dq_" : "mtk_attn_bwd_dq_") + dt + cz;
   q.grid = (unsigned)((long long)a.q_blocks * d.B * d.H);
-  q.block = 512;
+  q.block = wide ? 256 : 512;
   for (Launch *l : {&pre, &kv, &q}) {
     set_args(*l, a);
     p->launches.push_back(*l);

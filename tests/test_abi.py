@@ -300,9 +300,15 @@ def test_attention_select_and_validation():
         with pytest.raises(mtk.MtkError) as e:
             mtk.AttentionPlan(None, 1, 1, 16, 16, D, q_rows=q_rows)
         assert e.value.status == status
-    with pytest.raises(mtk.MtkError) as e:  # the backward: D = 128 only
-        mtk.AttentionBwdPlan(None, 1, 1, 16, 16, 64)
-    assert e.value.status == mtk.MTK_ERR_UNSUPPORTED
+    for D in (60, 264, 0):  # the backward: multiples of 8 up to 256
+        with pytest.raises(mtk.MtkError) as e:
+            mtk.AttentionBwdPlan(None, 1, 1, 16, 16, D)
+        assert e.value.status == mtk.MTK_ERR_UNSUPPORTED
+    # D <= 128: 128-key dK/dV and 256-query dQ workgroups; D > 128: 64 keys / 64 queries per workgroup
+    assert "grids=32/4/2 " in mtk.AttentionBwdPlan(None, 1, 2, 256, 200, 64).describe() + " "
+    b = mtk.AttentionBwdPlan(None, 1, 2, 256, 200, 256, causal=True)
+    assert "grids=32/8/8 " in b.describe() + " " and b.describe().endswith(
+        "kernels: mtk_attn_bwd_pre_f16 mtk_attn_bwd256_dkdv_f16_causal mtk_attn_bwd256_dq_f16_causal")
     with pytest.raises(mtk.MtkError) as e:
         mtk.AttentionPlan(None, 0, 1, 16, 16, 128)
     assert e.value.status == mtk.MTK_ERR_INVALID

@@ -66,11 +66,10 @@ def _check(name, got, exp, bound_terms, dtype):
     assert worst <= 1.0, (name, worst)
 
 
-def _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=90, pairs=None, Hkv=None):
+def _run_and_check(dev, B, H, Sq, Skv, causal, dtype, seed=90, pairs=None, Hkv=None, D=128):
     """GPU forward (for O and lse) and backward once, then the oracle check: on every (b, h) pair,
     or, with `pairs` (a list of [p0, p1) ranges of flattened b * H + h), on those pairs chunk by
     chunk (the float64 bound terms cost S_q * S_kv memory per pair)."""
-    D = 128
     Hkv = Hkv or H
     group = H // Hkv
     print(f"[attn bwd] B={B} H={H} H_kv={Hkv} S_q={Sq} S_kv={Skv} causal={causal} {dtype} pairs={pairs}", flush=True)
@@ -186,9 +185,10 @@ def test_attention_bwd_constant_v_rows(dev):
 
 
 def test_attention_bwd_errors(dev):
-    with pytest.raises(mtk.MtkError) as e:
-        mtk.AttentionBwdPlan(dev, 1, 1, 64, 64, D=64)
-    assert e.value.status == mtk.MTK_ERR_UNSUPPORTED
+    for D in (60, 264):  # head dimensions: multiples of 8 up to 256
+        with pytest.raises(mtk.MtkError) as e:
+            mtk.AttentionBwdPlan(dev, 1, 1, 64, 64, D=D)
+        assert e.value.status == mtk.MTK_ERR_UNSUPPORTED
     plan = mtk.AttentionBwdPlan(dev, 1, 1, 64, 64)
     assert plan.workspace_bytes >= 64 * 4
     buf = dev.empty(64 * 128 * 2)
