@@ -445,8 +445,8 @@ def main():
                     "config 5 shape with 8 K/V heads (H=32, H_kv=8), flash-attn backward", pgb, tm, "mfma",
                     key="config5_bwd_gqa8")
             # other head dimensions at the config 5 shape (the reference's run(headDimension:),
-            # attention.swift:398): D = 64 and D = 256, both masks
-            for hd in (64, 256):
+            # attention.swift:398): D = 64, 256 and 512, both masks; the backward at D = 64 and 256
+            for hd in (64, 256, 512):
                 if not want(f"config5_attn_d{hd}"):
                     continue
                 shp_d = (2, 4096, 32, hd)
@@ -461,6 +461,8 @@ def main():
                     key = f"config5_attn_d{hd}" + ("_causal" if causal else "")
                     cfgs[key] = summarize(f"config 5 shape, head dimension {hd}, flash-attn fwd "
                                           f"{'causal' if causal else 'non-causal'}", pd, tm, "mfma", key=key)
+                if hd > 256:  # the backward takes head dimensions up to 256
+                    continue
                 # the backward at this head dimension (non-causal): O and lse from the forward
                 pdf = mtk.AttentionPlan(dev, 2, 32, 4096, 4096, hd)
                 pdb = mtk.AttentionBwdPlan(dev, 2, 32, 4096, 4096, hd)

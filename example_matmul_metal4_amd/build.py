@@ -24,7 +24,7 @@ CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
-HIP_UNITS = ["gemm_f16", "gemm_bf16", "conv", "attention", "attention_hd", "attention_bwd", "attention_bwd256", "skinny",
+HIP_UNITS = ["gemm_f16", "gemm_bf16", "conv", "attention", "attention_hd", "attention_bwd", "attention_bwd256", "attention_wide", "skinny",
              "permute", "util"]
 
 HIPCC_FLAGS = [

@@ -49,7 +49,7 @@ int fail(int status, const char *fmt, ...) {
 
 constexpr uint64_t kMaxOperandBytes = (1ull << 31) - 256;  // buffer-resource ranges (see device.hpp)
 constexpr int kAutoKStagger = 16;  // in-workgroup split-K: boundary offsets span up to 16 K-tiles
-constexpr int kMaxHeadDim = MTK_ATTN_MAX_HEAD_DIM;  // largest padded head dimension compiled (256)
+constexpr int kMaxHeadDim = MTK_ATTN_MAX_HEAD_DIM;  // largest padded head dimension compiled (512)
 
 }  // namespace
 
@@ -746,6 +746,12 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
     return fail(MTK_ERR_INVALID, "H_kv must divide H (got H=%d, H_kv=%d)", d.H, d.H_kv);
   if (d.D < 1 || d.D > kMaxHeadDim)
     return fail(MTK_ERR_UNSUPPORTED, "head dimension must be 1..%d (got %d)", kMaxHeadDim, d.D);
+  // above 256: the 16-query wavefront kernel laid out for 512 (16-byte aligned rows only)
+  const bool wide = d.D > 256;
+  if (wide && d.D % 8 != 0)
+    return fail(MTK_ERR_UNSUPPORTED, "head dimensions above 256 must be multiples of 8 (got %d)", d.D);
+  if (wide && d.q_rows != 0)
+    return fail(MTK_ERR_UNSUPPORTED, "head dimensions above 256 run 64 query rows per workgroup (q_rows must be 0)");
   if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "attention dtype must be MTK_F16 or MTK_BF16");
   if (d.q_rows != 0 && d.q_rows != 128 && d.q_rows != 256)
     return fail(MTK_ERR_INVALID, "q_rows must be 0, 128 or 256 (got %d)", d.q_rows);
@@ -762,7 +768,7 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   // Head dimension: the kernels are compiled for a padded head dimension DP of 64, 128 or 256 and
   // run any D <= DP. D % 8 == 0 keeps every row 16-byte aligned (direct-to-LDS staging, 16-byte
   // loads); other D use the element-staged kernels (2-byte aligned rows).
-  const int dp = d.D <= 64 ? 64 : d.D <= 128 ? 128 : 256;
+  const int dp = d.D <= 64 ? 64 : d.D <= 128 ? 128 : d.D <= 256 ? 256 : 512;
   const bool gen = d.D % 8 != 0;
   p->align_a = p->align_b = gen ? 2 : 16;
   // Query rows per workgroup: 256 (the ping-pong kernel: 8 wavefronts in two groups alternating MFMA
@@ -774,6 +780,7 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   if (rows == 0) {
     const int cus = ctx ? ctx->prop.multiProcessorCount : 256;
     rows = (d.D == 128 && !d.causal && (long long)d.B * d.H * ((d.S_q + 255) / 256) >= cus) ? 256 : 128;
+    if (wide) rows = 64;
   }
   Launch g;
   std::string family = rows == 256 ? "pp_" : "";

@@ -172,12 +172,14 @@ int mtk_gemm_run_noalloc(const mtk_plan *plan, const mtk_gemm_args *args);
  * constants (Sources/attention/attention.swift:9-21, 117-120, 423-431).
  * Q, O: [B][S_q][H][D]; K, V: [B][S_kv][H_kv][D] (the reference's [S][H][D] packing,
  * attention.swift:466-468, with a batch dimension). scale = 1/sqrt(D).
- * D (the reference's K, the head dimension: attention.swift:17, 398) is any value from 1 to
- * MTK_ATTN_MAX_HEAD_DIM. The reference covers any K with 128-wide blocks and a masked remainder
- * block (attention.swift:25, 84-91, 192-199); here the forward kernels are compiled for a padded
- * head dimension of 64, 128 or 256 and zero the dims past D. D % 8 == 0 needs 16-byte aligned
- * Q, K, V, O; other D only 2-byte alignment (element-staged kernels, slower). The backward plan
- * supports D = 128 only (MTK_ERR_UNSUPPORTED otherwise).
+ * D (the reference's K, the head dimension: attention.swift:17, 398) is any value from 1 to 256
+ * and any multiple of 8 up to MTK_ATTN_MAX_HEAD_DIM (512). The reference covers any K with
+ * 128-wide blocks and a masked remainder block (attention.swift:25, 84-91, 192-199); here the
+ * forward kernels are compiled for a padded head dimension of 64, 128, 256 or 512 and zero the
+ * dims past D. D % 8 == 0 needs 16-byte aligned Q, K, V, O; other D (up to 256) only 2-byte
+ * alignment (element-staged kernels, slower). D above 256 runs 64 query rows per workgroup
+ * (q_rows must be 0). The backward plan supports every multiple of 8 up to 256
+ * (MTK_ERR_UNSUPPORTED otherwise).
  * H_kv (appended; 0 = H) is the reference's Hk: H must be a multiple of it and query head h reads
  * K/V head h / (H / H_kv) (grouped-query attention). The reference declares Hk (attention.swift:20,
  * 131) but slices K and V at the query head (attention.swift:156), so it defines only Hq == Hk,
@@ -186,7 +188,7 @@ int mtk_gemm_run_noalloc(const mtk_plan *plan, const mtk_gemm_args *args);
  * q_rows: query rows per workgroup, 0 = let the plan choose; 128 (4 wavefronts of 32 queries, two
  * workgroups per CU) or 256 (8 wavefronts of 32 queries in two groups that alternate MFMA and
  * softmax blocks, one workgroup per CU; D = 128 only). Same results bit for bit. */
-#define MTK_ATTN_MAX_HEAD_DIM 256
+#define MTK_ATTN_MAX_HEAD_DIM 512
 
 typedef struct {
   int B, H, S_q, S_kv, D;

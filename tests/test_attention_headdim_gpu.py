@@ -3,8 +3,9 @@ against the CPU oracle (Network.swift:134-179, 286-311, which takes any head dim
 
 The reference's generator and run(headDimension:) accept any head dimension K
 (Sources/attention/attention.swift:25 kBlocks, 84-91 masked remainder store, 192-199 remainder
-block of the Q.K^T walk, 398). The kernels here are compiled for padded head dimensions 64, 128 and
-256; head dimensions that are not a multiple of 8 run the element-staged kernels.
+block of the Q.K^T walk, 398). The kernels here are compiled for padded head dimensions 64, 128,
+256 and 512 (the last: multiples of 8 above 256, 16 queries per wavefront); head dimensions up to
+256 that are not a multiple of 8 run the element-staged kernels.
 
 Acceptance as in test_attention_gpu.py: relative Frobenius <= 1e-3 (f16 out) and element-wise
 |y - yhat| <= ulp_out(|yhat|) + 2^-10 * sum_j P_ij |V_jd| (bf16: 2^-7 and its rounding floor)."""
@@ -17,8 +18,8 @@ from test_attention_gpu import _probs_rows_f64, check
 
 pytestmark = pytest.mark.gpu
 
-# multiples of 8 (direct-to-LDS kernels padded to 64 / 128 / 256) and others (element-staged)
-FAST_D = [8, 40, 64, 72, 96, 120, 136, 200, 256]
+# multiples of 8 (direct-to-LDS kernels padded to 64 / 128 / 256 / 512) and others (element-staged)
+FAST_D = [8, 40, 64, 72, 96, 120, 136, 200, 256, 264, 384, 504, 512]
 GEN_D = [1, 3, 17, 63, 65, 100, 129, 255]
 
 
@@ -36,7 +37,7 @@ def test_head_dim_sweep(dev, D, causal):
 
 
 @pytest.mark.parametrize("S", [1, 63, 64, 65, 129, 1000])
-@pytest.mark.parametrize("D", [64, 96, 256, 100])
+@pytest.mark.parametrize("D", [64, 96, 256, 100, 320])
 @pytest.mark.parametrize("causal", [False, True])
 def test_head_dim_sequence_sweep(dev, S, D, causal):
     # profileCorrectness's S sweep (attention.swift:391-396) at other head dimensions
@@ -44,14 +45,14 @@ def test_head_dim_sequence_sweep(dev, S, D, causal):
     check(dev, Q, K, V, causal, label=f"D{D} S{S}")
 
 
-@pytest.mark.parametrize("D", [64, 256, 33])
+@pytest.mark.parametrize("D", [64, 256, 33, 512])
 @pytest.mark.parametrize("causal", [False, True])
 def test_head_dim_bf16(dev, D, causal):
     Q, K, V = qkv_d(40, 2, 333, 2, D, dtype="bf16")
     check(dev, Q, K, V, causal, dtype="bf16", label=f"bf16 D{D}")
 
 
-@pytest.mark.parametrize("D", [64, 256, 100])
+@pytest.mark.parametrize("D", [64, 256, 100, 448])
 @pytest.mark.parametrize("causal", [False, True])
 def test_head_dim_grouped_kv(dev, D, causal):
     # grouped K/V heads: same bits as K/V repeated over each group
@@ -61,7 +62,7 @@ def test_head_dim_grouped_kv(dev, D, causal):
     assert np.array_equal(got.view(np.uint16), full.view(np.uint16))
 
 
-@pytest.mark.parametrize("D", [64, 96, 256, 37])
+@pytest.mark.parametrize("D", [64, 96, 256, 37, 512])
 def test_head_dim_closed_forms(dev, D):
     B, S, H = 1, 200, 2
     Q, K, _ = qkv_d(90, B, S, H, D)
@@ -75,8 +76,8 @@ def test_head_dim_closed_forms(dev, D):
 
 
 def test_head_dim_lse(dev):
-    # the forward's row log-sum-exp at D = 64 and D = 100 against float64
-    for D in (64, 100):
+    # the forward's row log-sum-exp at D = 64, 100 and 384 against float64
+    for D in (64, 100, 384):
         Q, K, V = qkv_d(95, 1, 150, 2, D)
         _, lse = mtk.attention(dev, Q, K, V, causal=True, return_lse=True)
         s = np.einsum("bihd,bjhd->bhij", Q.astype(np.float64), K.astype(np.float64)) / np.sqrt(D)
@@ -107,14 +108,17 @@ def test_odd_head_dim_unaligned_pointers(dev):
 
 
 def test_head_dim_limits(dev):
-    with pytest.raises(mtk.MtkError):
-        mtk.AttentionPlan(dev, 1, 1, 16, 16, 257)
-    with pytest.raises(mtk.MtkError):
-        mtk.AttentionPlan(dev, 1, 1, 16, 16, 0)
+    for D in (257, 300 + 1, 520, 0):  # above 256 only multiples of 8, up to 512
+        with pytest.raises(mtk.MtkError) as e:
+            mtk.AttentionPlan(dev, 1, 1, 16, 16, D)
+        assert e.value.status == mtk.MTK_ERR_UNSUPPORTED
     with pytest.raises(mtk.MtkError):  # the ping-pong kernel is for D = 128 only
         mtk.AttentionPlan(dev, 1, 1, 16, 16, 64, q_rows=256)
-    with pytest.raises(mtk.MtkError):  # the backward supports D = 128 only
-        mtk.AttentionBwdPlan(dev, 1, 1, 16, 16, 64)
+    with pytest.raises(mtk.MtkError):  # D above 256: 64 query rows per workgroup, chosen by the plan
+        mtk.AttentionPlan(dev, 1, 1, 16, 16, 264, q_rows=128)
+    assert "rows/wg=64 " in mtk.AttentionPlan(dev, 1, 2, 100, 100, 512).describe()
+    with pytest.raises(mtk.MtkError):  # the backward: multiples of 8 up to 256
+        mtk.AttentionBwdPlan(dev, 1, 1, 16, 16, 264)
     plan = mtk.AttentionPlan(dev, 1, 1, 16, 16, 24)  # D % 8 == 0: 16-byte alignment required
     buf = dev.empty(4096)
     with pytest.raises(mtk.MtkError):
@@ -122,7 +126,7 @@ def test_head_dim_limits(dev):
     buf.free()
 
 
-@pytest.mark.parametrize("D", [64, 96, 256])
+@pytest.mark.parametrize("D", [64, 96, 256, 512])
 def test_config5_shape_head_dims(dev, D):
     # config 5's shape (B=2, H=32, S=4096) at other head dimensions, both masks: 256 query rows of
     # every (b, h) per mask (4 blocks of 64 spread over the sequence, first and last included)
