@@ -134,7 +134,7 @@ __device__ __forceinline__ void attn_fwd_pp(const mtk_attn_kargs &a) {
   // ordinary LDS reads would wait for the K/V loads of later tiles in flight), issued kLook steps
   // ahead into a ring of registers; before its MFMAs a step waits until at most 2 * (steps issued
   // after it) reads are outstanding (LDS reads complete in order), its registers tied to the wait.
-  constexpr int kLook = 2, kRing = kLook + 2;
+  constexpr int kLook = 6, kRing = kLook + 2;
   auto mfma_block = [&](int k, auto pv_c, auto sk_c) {
     constexpr bool PV = decltype(pv_c)::value, SK = decltype(sk_c)::value;
     constexpr int kPerDb = (SK ? 2 : 0) + (PV ? 4 : 0), kSteps = 4 * kPerDb;
