@@ -178,6 +178,17 @@ __device__ __forceinline__ u32x4 ds_read_b128_at(uint32_t addr) {
   return w;
 }
 
+// 16-byte LDS read / write as inline asm at a byte address (the caller waits for the read with an
+// lgkmcnt wait that carries its registers), for code that keeps direct-to-LDS loads in flight.
+__device__ __forceinline__ u32x4 lds_rd128(uint32_t addr) {
+  u32x4 w;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(w) : "v"(addr));
+  return w;
+}
+__device__ __forceinline__ void lds_wr128(uint32_t addr, u32x4 v) {
+  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+
 // Direct-to-LDS load with a uniform scalar offset added to the per-lane offset. The buffer range
 // check does not cover the scalar part: only for ranges known to lie inside the buffer.
 __device__ __forceinline__ void lds_direct16_s(rsrc_t r, char *lds, uint32_t voff, uint32_t soff) {
