@@ -13,12 +13,14 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 
-def _run_both(dev, M, N, K, split_k, split_mode, seed):
+def _run_both(dev, M, N, K, split_k, split_mode, seed, expect=None):
     A = oracle.normal(seed, (M, K), 0, 1 / np.sqrt(K))
     B = oracle.normal(seed + 1, (N, K), 0, 1 / np.sqrt(K))
     bias = oracle.uniform(seed + 2, (N,), -0.5, 0.5)
     plan = mtk.GemmPlan(dev, M, N, K, trans_b=True, has_bias=True, split_k=split_k, split_mode=split_mode)
     print(f"[noalloc] {plan.describe()} workspace={plan.workspace_bytes}", flush=True)
+    if expect:
+        assert expect in plan.describe(), plan.describe()
     assert 0 < plan.workspace_bytes <= (64 << 20)
     dA, dB, dbias = dev.upload(A), dev.upload(B), dev.upload(bias)
     c_ref, c_na = dev.empty(M * N * 2), dev.empty(M * N * 2)
@@ -48,6 +50,14 @@ def test_noalloc_matches_run_two_calls(dev, split_mode):
     else:  # two-pass: fp32 partials [split_k][M][N], then the reduce kernel
         _run_both(dev, 1024, 1536, 2100, 8, split_mode, 30)
         _run_both(dev, 200, 300, 900, 4, split_mode, 40)
+
+
+def test_noalloc_skinny_partials(dev):
+    # the partial-writing skinny kernel (16 < M <= 32, long K: the reference's default run
+    # M=32, N=3072, K=80000, split-K 30, matmul.swift:334) sets its partial pointer on its own launch
+    # path; 30 fp32 partials of 32 x 3072 (11.8 MB) in the static scratch, then a smaller problem
+    _run_both(dev, 32, 3072, 80000, 30, "auto", 60, expect="skinny partials")
+    _run_both(dev, 24, 1000, 9000, 6, "auto", 70, expect="skinny partials")
 
 
 def test_noalloc_config2_full_size(dev):
