@@ -178,6 +178,14 @@ __device__ __forceinline__ u32x4 ds_read_b128_at(uint32_t addr) {
   return w;
 }
 
+// The same read into the registers that hold dst (an in/out operand: the compiler keeps the new
+// value where the old one was, e.g. a fragment re-read right after its last use).
+template <int OFF>
+__device__ __forceinline__ void ds_read_b128_into(u32x4 &dst, uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "+v"(dst) : "v"(addr), "i"(OFF));
+}
+
 // 16-byte LDS read / write as inline asm at a byte address (the caller waits for the read with an
 // lgkmcnt wait that carries its registers), for code that keeps direct-to-LDS loads in flight.
 __device__ __forceinline__ u32x4 lds_rd128(uint32_t addr) {

@@ -79,7 +79,10 @@ struct OpRows {
   // K offset of the fragment a lane reads for k-step ks of K-tile kt
   __device__ static __forceinline__ int frag_k0(int kt, int ks, int lane) { return kt * kBK + 16 * ks + 8 * (lane >> 5); }
   __device__ __forceinline__ u32x4 frag(const char *lds, int rowblk, int ks, int lane) const {
-    return ds_read_b128_at<0>(lds_addr(lds) + lds_off(rowblk + (lane & 31), 2 * ks + (lane >> 5)));
+    return ds_read_b128_at<0>(lds_addr(lds) + frag_off(rowblk, ks, lane));
+  }
+  __device__ __forceinline__ void frag_to(u32x4 &dst, const char *lds, int rowblk, int ks, int lane) const {
+    ds_read_b128_into<0>(dst, lds_addr(lds) + frag_off(rowblk, ks, lane));
   }
 };
 
@@ -144,7 +147,10 @@ struct OpConv {
     lds_direct16(r, lds + (blk0 + q) * 1024, ok ? (uint32_t)(pb8[q] + tp.elems) * 2u : kOOB);
   }
   __device__ __forceinline__ u32x4 frag(const char *lds, int rowblk, int ks, int lane) const {
-    return ds_read_b128_at<0>(lds_addr(lds) + lds_off(rowblk + (lane & 31), 2 * ks + (lane >> 5)));
+    return ds_read_b128_at<0>(lds_addr(lds) + frag_off(rowblk, ks, lane));
+  }
+  __device__ __forceinline__ void frag_to(u32x4 &dst, const char *lds, int rowblk, int ks, int lane) const {
+    ds_read_b128_into<0>(dst, lds_addr(lds) + frag_off(rowblk, ks, lane));
   }
 };
 
@@ -176,6 +182,9 @@ struct OpColsT {
   }
   __device__ __forceinline__ void issue(rsrc_t r, char *lds, int q, int kt) const {
     lds_direct16(r, lds + (blk0 + q) * 1024, off[q] + (uint32_t)kt * kstride);
+  }
+  __device__ __forceinline__ void frag_to(u32x4 &dst, const char *lds, int colblk, int ks, int lane) const {
+    dst = frag(lds, colblk, ks, lane);
   }
   __device__ __forceinline__ u32x4 frag(const char *lds, int colblk, int ks, int lane) const {
     const int s = lane & 15, h = lane >> 4;
@@ -238,10 +247,10 @@ __device__ __forceinline__ void frag_wait(u32x4 (&fa)[TA], u32x4 (&fb)[TB]) {
 // SERIAL (GEMM split-K on a tile grid that already fills the chip, at most 4 partitions): one
 // workgroup per output tile runs the K partitions one after another through one continuous
 // pipeline. At the end of each partition but the last its fp32 sum is added to the tile's running
-// sum (in the workspace; one accumulator block per wavefront in LDS) and the accumulators restart
-// from zero; the epilogue adds the running sum and the last partition, then the bias. The arithmetic is the two-pass split-K's: every partition
-// accumulates from zero over the same K-tiles, partition sums are added in partition order, the
-// bias last.
+// sum (part in the workspace, part in registers, one accumulator block per wavefront in LDS) and
+// the accumulators restart from zero; the epilogue adds the running sum and the last partition,
+// then the bias. The arithmetic is the two-pass split-K's: every partition accumulates from zero
+// over the same K-tiles, partition sums are added in partition order, the bias last.
 template <int DT, int BM, int BN, int WAVES_M, int WAVES_N, typename AOP, typename BOP, bool SERIAL = false>
 __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   constexpr int NW = WAVES_M * WAVES_N;
@@ -258,9 +267,18 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   constexpr int kPerGroup = (PA + PB + kLoadGroups - 1) / kLoadGroups;
   constexpr int kReadsPerGroup = (TM + TN + TM - 1) / TM;  // next k-step's fragment reads per MFMA group
 
-  // SERIAL: the last accumulator block of every wavefront keeps its running sum in LDS past the two
-  // stages (4 KB per wavefront: 32 KB at 256x256, which fills the 160 KB of LDS), not in the slot
+  // The K loop: fragments two k-steps ahead through a ring of four k-step buffers, or (256x256
+  // convolution and split-K) one k-step ahead through two.
+  constexpr bool kOneAhead = BM == 256 && (AOP::kIsConv || SERIAL);
+  // SERIAL: where each wavefront's running sum lives, by accumulator block b = i + TM * j: blocks
+  // b < kSlotBlocks in the workspace slot, the next kRegBlocks in registers (the registers the
+  // fragments leave free: three blocks at 256x256 with the one-ahead loop, two at 128x128), the last
+  // one, (TM - 1, TN - 1), in LDS past the two stages (4 KB per wavefront: 32 KB at 256x256, which
+  // fills the 160 KB of LDS).
   constexpr int kLdsBlocks = SERIAL ? 1 : 0;
+  constexpr int kRegBlocks = SERIAL ? (BM == 256 ? 3 : 2) : 0;
+  constexpr int kSlotBlocks = SERIAL ? TM * TN - kLdsBlocks - kRegBlocks : 0;
+  static_assert(kSlotBlocks >= 0, "running-sum blocks");
   constexpr int kLdsRun = kLdsBlocks * NW * 4096;
   static_assert(2 * kStage + kLdsRun <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) char smem[2 * kStage + kLdsRun];
@@ -320,9 +338,11 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   // partition 0; later ones add the finished partition to the slot ((p0 + p1) + p2 ...); the
   // epilogue adds the slot in front of the last partition. Slot loads bypass L1 (device scope), so
   // a line read at one boundary is never served stale at the next. The last block (TM - 1, TN - 1)
-  // of every wavefront keeps its running sum in the LDS left over by the two stages instead (the
-  // same additions in the same order): one eighth less slot traffic at 256x256 (config 2 split-K 4:
-  // 196.7 -> 191.0 us median, one process, same bits).
+  // of every wavefront keeps its running sum in the LDS left over by the two stages instead, and
+  // the kRegBlocks blocks before it in registers (the same additions in the same order): at
+  // 256x256 half of the running sum never leaves the CU (config 2 split-K 4: 196.7 us with all of
+  // it in the slot, 191.0 with the LDS block, 176.4 with three register blocks as well and the
+  // one-ahead loop; medians, one process, same bits).
   constexpr uint32_t kSlotBytes = BM * BN * 4;
   // Slot traffic is streamed: sc1 (device scope: loads are served by L2, never by a possibly stale
   // L1 line) + nt on stores and loads alike, which keeps it from displacing the A/B panels the
@@ -351,11 +371,88 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rslot, slot_lane, slot_blk(i, j, q), kLoadPolicy));
   };
   int split_end = SERIAL ? split_first_tile(a, 1, t) : 0;  // SERIAL: first K-tile of the next partition
-  int parked = 0;                                           // SERIAL: partitions parked in the workspace
-  constexpr int kSlotStores = (TM * TN - kLdsBlocks) * 4;  // slot store instructions per wavefront and boundary
+  int parked = 0;                                           // SERIAL: partitions parked so far
+  constexpr int kSlotStores = kSlotBlocks * 4;  // slot store instructions per wavefront and boundary
   static_assert(!SERIAL || kSlotStores < 64, "vmcnt range");
+  // SERIAL: running sums of the register-resident accumulator blocks (set at the first boundary,
+  // read only after one)
+  f32x16 run[kRegBlocks > 0 ? kRegBlocks : 1];
 
-  if constexpr (!AOP::kIsConv || BM == 128) {
+  // SERIAL, at a partition boundary (every LDS read of the loop waited for): running sum += the
+  // finished partition's sum (partition 0's sum as it is), accumulators back to zero.
+  auto park = [&]() {
+    const uint32_t slot_lane = slot_lane_at();
+    // the LDS-resident block (TM - 1, TN - 1), in place (inline asm: ordinary LDS accesses would
+    // wait for the next partition's K-tile loads in flight)
+    if constexpr (kLdsBlocks > 0) {
+      const uint32_t la = lds_run_at();
+      constexpr int I = TM - 1, J = TN - 1;
+      if (parked > 0) {
+        // one register quad at a time (the boundary is where registers are scarcest)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          u32x4 prev = lds_rd128(la + 1024u * q);
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(prev));
+          const f32x4 v = __builtin_bit_cast(f32x4, prev) +
+                          f32x4{acc[I][J][4 * q], acc[I][J][4 * q + 1], acc[I][J][4 * q + 2], acc[I][J][4 * q + 3]};
+          lds_wr128(la + 1024u * q, __builtin_bit_cast(u32x4, v));
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          lds_wr128(la + 1024u * q, __builtin_bit_cast(u32x4, f32x4{acc[I][J][4 * q], acc[I][J][4 * q + 1],
+                                                                    acc[I][J][4 * q + 2], acc[I][J][4 * q + 3]}));
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    // the register-resident blocks
+#pragma unroll
+    for (int r = 0; r < kRegBlocks; ++r) {
+      const int b = kSlotBlocks + r;
+      run[r] = parked > 0 ? run[r] + acc[b % TM][b / TM] : acc[b % TM][b / TM];
+    }
+    // the slot blocks
+    if (parked == 0) {
+#pragma unroll
+      for (int b = 0; b < kSlotBlocks; ++b)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x16 &s = acc[b % TM][b / TM];
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4, f32x4{s[4 * q], s[4 * q + 1], s[4 * q + 2], s[4 * q + 3]}), rslot, slot_lane,
+              slot_blk(b % TM, b / TM, q), kStorePolicy);
+        }
+    } else {
+      // one register quad (16 bytes per lane) at a time, the next kAheadQ quads' loads in flight
+      constexpr int kQuads = kSlotBlocks * 4, kAheadQ = 3;
+      auto quad_load = [&](int x) { return slot_load(slot_lane, (x / 4) % TM, (x / 4) / TM, x % 4); };
+      f32x4 ring[kAheadQ + 1];
+#pragma unroll
+      for (int x = 0; x < kAheadQ && x < kQuads; ++x) ring[x] = quad_load(x);
+#pragma unroll
+      for (int x = 0; x < kQuads; ++x) {
+        const int i = (x / 4) % TM, j = (x / 4) / TM, q = x % 4;
+        if (x + kAheadQ < kQuads) ring[(x + kAheadQ) % (kAheadQ + 1)] = quad_load(x + kAheadQ);
+        const f32x4 v = ring[x % (kAheadQ + 1)] +
+                        f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rslot, slot_lane, slot_blk(i, j, q),
+                                               kStorePolicy);
+      }
+    }
+    ++parked;
+    split_end = split_first_tile(a, parked + 1, t);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
+  };
+  // SERIAL: the K loop runs once per partition (the pipeline carries on across the boundary).
+  // Partition boundaries lie strictly inside K (at most split_k-1 of them); the K loop ends anywhere
+  // else (or at K itself) after the last partition. Only boundaries park, so every slot written is
+  // one of this tile's split_k-1.
+  auto at_boundary = [&](int kt) { return kt == split_end && split_end < a.k_tiles && parked < a.split_k - 1; };
+
+  if constexpr (!kOneAhead) {
     // Fragments: a ring of four k-step buffers (slot s holds k-step s of a K-tile), read two k-steps
     // ahead. The reads are inline asm, which the compiler does not track: it would otherwise make
     // every LDS read wait for the direct-to-LDS loads in flight, and at the loop's back edge for
@@ -453,8 +550,6 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       });
     };
 
-    // SERIAL: the K loop runs once per partition (the pipeline carries on across the boundary); the
-    // partition sum is parked between the runs.
     int kt = kt0;
     bool pre = false;
     for (;;) {
@@ -467,82 +562,11 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       if constexpr (!SERIAL) {
         break;
       } else {
-        // Partition boundaries lie strictly inside K (at most split_k-1 of them); the K loop ends
-        // anywhere else (or at K itself) after the last partition. Only boundaries park, so every
-        // slot written is one of this tile's split_k-1.
-        if (kt != split_end || split_end >= a.k_tiles || parked >= a.split_k - 1) break;
+        if (!at_boundary(kt)) break;
         pre = true;
         frag_wait<0>(fa[0], fb[0]);
         frag_tie(fa[1], fb[1]);
-        const uint32_t slot_lane = slot_lane_at();
-        // the LDS-resident block (TM - 1, TN - 1): running sum += partition sum in place (inline
-        // asm: ordinary LDS accesses would wait for the next partition's K-tile loads in flight)
-        if constexpr (kLdsBlocks > 0) {
-          const uint32_t la = lds_run_at();
-          constexpr int I = TM - 1, J = TN - 1;
-          if (parked > 0) {
-            u32x4 prev[4];
-  #pragma unroll
-            for (int q = 0; q < 4; ++q) prev[q] = lds_rd128(la + 1024u * q);
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(prev[0]), "+v"(prev[1]), "+v"(prev[2]), "+v"(prev[3]));
-  #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const f32x4 v = __builtin_bit_cast(f32x4, prev[q]) +
-                              f32x4{acc[I][J][4 * q], acc[I][J][4 * q + 1], acc[I][J][4 * q + 2], acc[I][J][4 * q + 3]};
-              lds_wr128(la + 1024u * q, __builtin_bit_cast(u32x4, v));
-            }
-          } else {  // partition 0's sum as it is
-  #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              lds_wr128(la + 1024u * q, __builtin_bit_cast(u32x4, f32x4{acc[I][J][4 * q], acc[I][J][4 * q + 1],
-                                                                        acc[I][J][4 * q + 2], acc[I][J][4 * q + 3]}));
-          }
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        }
-        if (parked == 0) {
-  #pragma unroll
-          for (int i = 0; i < TM; ++i)
-  #pragma unroll
-            for (int j = 0; j < TN; ++j) {
-              if (kLdsBlocks > 0 && i == TM - 1 && j == TN - 1) continue;
-  #pragma unroll
-              for (int q = 0; q < 4; ++q)
-                __builtin_amdgcn_raw_buffer_store_b128(
-                    __builtin_bit_cast(u32x4, f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                                                    acc[i][j][4 * q + 3]}),
-                    rslot, slot_lane, slot_blk(i, j, q), kStorePolicy);
-            }
-        } else {
-          // slot += partition sum, one accumulator block at a time, the next kSlotRing-1 blocks'
-          // loads in flight
-          f32x4 ring[kSlotRing][4];
-  #pragma unroll
-          for (int b = 0; b + 1 < kSlotRing; ++b)
-  #pragma unroll
-            for (int q = 0; q < 4; ++q) ring[b][q] = slot_load(slot_lane, b % TM, b / TM, q);
-  #pragma unroll
-          for (int b = 0; b < TM * TN - kLdsBlocks; ++b) {
-            const int i = b % TM, j = b / TM;
-            constexpr int kAhead = kSlotRing - 1;
-            if (b + kAhead < TM * TN - kLdsBlocks) {
-  #pragma unroll
-              for (int q = 0; q < 4; ++q) ring[(b + kAhead) % kSlotRing][q] = slot_load(slot_lane, (b + kAhead) % TM, (b + kAhead) / TM, q);
-            }
-  #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const f32x4 v = ring[b % kSlotRing][q] +
-                              f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rslot, slot_lane, slot_blk(i, j, q),
-                                                     kStorePolicy);
-            }
-          }
-        }
-        ++parked;
-        split_end = split_first_tile(a, parked + 1, t);
-  #pragma unroll
-        for (int i = 0; i < TM; ++i)
-  #pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
+        park();
       }
     }
     // The reads of the last K-tile's k-steps 2 and 3 (fragments of the partial last K-tile, or of a
@@ -577,80 +601,207 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       }
     }
   } else {
-    // 256x256 convolution: fragments one k-step ahead (two buffers); the loads of K-tile kt + 1 go
-    // out in the first MFMA groups of K-tile kt and are waited for at one barrier before its last
-    // k-step. (The two-ahead ring measured 2-5 % slower on this gather, whose loads of K-tile kt + 2
-    // then come in the second half of K-tile kt; on the 128x128 convolution it is 1-2 % faster.)
-    // K-tiles are visited channel-block-major: all filter taps of channels 0..63, then of 64..127,
-    // and so on (K-tile kt of the visit is tap kt % T of channel block kt / T, i.e. K-tile
-    // (kt % T) * (C / 64) + kt / T of the tap-major K order the operands are laid out in). The
-    // gather's reuse distance is shorter than tap-major (neighbouring taps read overlapping pixel
-    // windows one after the other): conv2d 177.9 -> 172.1 us, the reference's 512-channel conv2d
-    // profile shape 336.8 -> 324.8 us. (With 128 channels, as at config 4b's 128x128 tiles, tap-major
-    // measured faster: both halves of a pixel's 256-byte channel row are then read back to back.)
-    static_assert(!SERIAL && !kAnyTail, "convolutions never split K and have whole K-tiles");
-    const int taps = a.cKD * a.cKH * a.cKW, cblocks = a.cC / kBK;
-    auto kmap = [&](int kt) { return (kt % taps) * cblocks + kt / taps; };
+    // 256x256 convolution and 256x256 in-workgroup split-K GEMM: fragments one k-step ahead; the
+    // loads of K-tile kt + 1 go out in the first MFMA groups of K-tile kt and are waited for at one
+    // barrier before its last k-step. Convolution: the two-ahead ring measured 2-5 % slower on this
+    // gather, whose loads of K-tile kt + 2 then come in the second half of K-tile kt (on the 128x128
+    // convolution it is 1-2 % faster). Split-K: the ring's fragments take 96 registers per lane,
+    // these 36, and the registers freed hold three accumulator blocks' running sums (so half of each
+    // wavefront's running sum never leaves the CU).
+    // Fragment registers: B fragments double-buffered by k-step parity; A fragment i of the next
+    // k-step is read into A fragment i's own register right after MFMA group i (the last use of
+    // it), so A takes TM registers plus one: A fragment TM - 1 of the last k-step of a K-tile goes
+    // to the spare (its regular register is still in use by group TM - 1 when the read is issued,
+    // in group TM - 2, early enough to be waited for with the barrier), and the next K-tile's
+    // A fragment TM - 1 goes back to its regular register in the last k-step's group 0. Each group
+    // waits (counted lgkmcnt, reads complete in issue order) for the reads it uses only.
+    // Convolution K-tiles are visited channel-block-major: all filter taps of channels 0..63, then
+    // of 64..127, and so on (K-tile kt of the visit is tap kt % T of channel block kt / T, i.e.
+    // K-tile (kt % T) * (C / 64) + kt / T of the tap-major K order the operands are laid out in).
+    // The gather's reuse distance is shorter than tap-major (neighbouring taps read overlapping
+    // pixel windows one after the other): conv2d 177.9 -> 172.1 us, the reference's 512-channel
+    // conv2d profile shape 336.8 -> 324.8 us. (With 128 channels, as at config 4b's 128x128 tiles,
+    // tap-major measured faster: both halves of a pixel's 256-byte channel row are then read back
+    // to back.)
+    static_assert(!AOP::kIsConv || (!SERIAL && !kAnyTail), "convolutions never split K and have whole K-tiles");
+    constexpr int kLast = kBK / 16 - 1;  // k-steps per K-tile - 1
+    static_assert(TM >= 3 && kLast == 3, "fragment schedule");
+    int taps = 1, cblocks = 1;
+    if constexpr (AOP::kIsConv) {
+      taps = a.cKD * a.cKH * a.cKW;
+      cblocks = a.cC / kBK;
+    }
+    auto kmap = [&](int kt) { return AOP::kIsConv ? (kt % taps) * cblocks + kt / taps : kt; };
     constexpr int kGroups1 = (kBK / 16) * TM;
     constexpr int kLoadGroups1 = 8 < kGroups1 - TM ? 8 : kGroups1 - TM;
     constexpr int kPerGroup1 = (PA + PB + kLoadGroups1 - 1) / kLoadGroups1;
+
+    // the register of k-step ks's A fragment i
+    constexpr auto areg = [](int ks, int i) { return ks == kLast && i == TM - 1 ? TM : i; };
+    // LDS read instructions issued by k-step p in MFMA group g (the fragments of k-step p + 1, the
+    // B fragments first in group 0)
+    constexpr int RA = AOP::kReadsPerFrag, RB = BOP::kReadsPerFrag;
+    constexpr auto nreads = [](int p, int g) {
+      if (p == kLast) return g == 0 ? TN * RB + 2 * RA : (g < TM - 1 ? RA : 0);
+      if (p == kLast - 1) return g == 0 ? TN * RB + RA : (g < TM - 2 ? RA : (g == TM - 2 ? 2 * RA : 0));
+      return g == 0 ? TN * RB + RA : RA;
+    };
+    // read instructions k-step p issues after the last one of k-step p + 1's A fragment i
+    constexpr auto later = [](int p, int i) {
+      const int slot = p == kLast ? (i == 0 ? 0 : (i == TM - 1 ? 1 : i + 1)) : i;  // A reads before it
+      return (TM - 1 - slot) * RA;
+    };
+    // lgkmcnt before MFMA group g of k-step c: the reads issued after the last one the group uses
+    // (B fragments and A fragment 0 in group 0, A fragment g later), by k-step c - 1 and by k-step
+    // c's earlier groups
+    constexpr auto wcount = [=](int c, int g) {
+      int n = later((c + kLast) % (kLast + 1), g);
+      for (int h = 0; h < g; ++h) n += nreads(c, h);
+      return n;
+    };
+    static_assert(wcount(0, TM - 1) <= 15 && wcount(1, TM - 1) <= 15, "lgkmcnt range");
+
+    u32x4 ga[TM + 1] = {}, gb[2][TN] = {};
+    auto tie = [](u32x4 &v) { asm volatile("" : "+v"(v)); };
+    auto tie_all = [&]() {
+#pragma unroll
+      for (int i = 0; i <= TM; ++i) tie(ga[i]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        tie(gb[0][j]);
+        tie(gb[1][j]);
+      }
+    };
+    // the reads k-step p issues in MFMA group g: fragments of k-step p + 1, at k-step index ksn of
+    // the stage at st
+    auto reads = [&](auto p_c, auto g_c, const char *st, int ksn) {
+      constexpr int p = decltype(p_c)::value, g = decltype(g_c)::value;
+      constexpr int n = (p + 1) % (kLast + 1);
+      auto rd_a = [&](int i) { opa.frag_to(ga[areg(n, i)], st, wave_m * WTM + i * 32, ksn, lane); };
+      if constexpr (g == 0) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) opb.frag_to(gb[n & 1][j], st + BM * 128, wave_n * WTN + j * 32, ksn, lane);
+        rd_a(0);
+        if constexpr (p == kLast) rd_a(TM - 1);
+      } else if constexpr (p == kLast) {
+        if constexpr (g < TM - 1) rd_a(g);
+      } else if constexpr (p == kLast - 1) {
+        if constexpr (g < TM - 1) rd_a(g);
+        if constexpr (g == TM - 2) rd_a(TM - 1);
+      } else {
+        rd_a(g);
+      }
+    };
+
     if (kt0 < kt1) issue_all(smem, kmap(kt0));
     wait_vmem();
     __syncthreads();
-    u32x4 ga[2][TM], gb[2][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) ga[0][i] = opa.frag(smem, wave_m * WTM + i * 32, 0, lane);
 #pragma unroll
     for (int j = 0; j < TN; ++j) gb[0][j] = opb.frag(smem + BM * 128, wave_n * WTN + j * 32, 0, lane);
-    for (int kt = kt0; kt < kt1; ++kt) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) ga[i] = opa.frag(smem, wave_m * WTM + i * 32, 0, lane);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    tie_all();
+
+    // One K-tile (TAIL: the partial last K-tile, with its first k-step's fragments read: masked at
+    // K, no loads, no reads past its last k-step). The barrier before the last k-step also waits
+    // for all of this K-tile's fragment reads (the next K-tile's loads overwrite its stage), and,
+    // after a partition boundary, for the slot stores issued before the loads. Past the end the
+    // last K-tile is reloaded (L2 hits, never computed) instead of a branch.
+    auto ktile1 = [&](const int kt, auto tail_c) {
+      constexpr bool TAIL = decltype(tail_c)::value;
       const int cur = (kt - kt0) & 1;
       char *nxt = smem + (cur ^ 1) * kStage;
-      // the last iteration reloads the current K-tile into the idle stage (L2 hits, never computed)
       const int kn = kmap(min(kt + 1, kt1 - 1));
       const char *sa = smem + cur * kStage;
-      const char *sb = sa + BM * 128;
-      const auto tp = opa.tap(a, kn);
+      typename std::conditional<AOP::kIsConv, typename OpConv<BM, NW>::Tap, int>::type tp{};
+      if constexpr (AOP::kIsConv) {
+        if constexpr (!TAIL) tp = opa.tap(a, kn);
+      }
       __builtin_amdgcn_sched_barrier(0);
+      static_for<0, kLast + 1>([&](auto k_c) {
+        constexpr int ks = decltype(k_c)::value;
+        constexpr int c = ks & 1;
+        const char *rs = ks < kLast ? sa : nxt;
+        constexpr int ksn = ks < kLast ? ks + 1 : 0;
+        static_for<0, TM>([&](auto i_c) {
+          constexpr int i = decltype(i_c)::value;
+          constexpr int ar = areg(ks, i);
+          if constexpr (TAIL) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            // the lane index taken afresh in each group: the masks are computed where they are used,
+            // not all at once ahead of the K-tile (which holds 16 more registers)
+            int ln = lane_id();
+            asm volatile("" : "+v"(ln));
+            tie(ga[ar]);
+            if constexpr (AOP::kNeedsTail) ga[ar] = AOP::mask(ga[ar], AOP::frag_k0(kt, ks, ln), a.K);
+            if constexpr (i == 0) {
 #pragma unroll
-      for (int ks = 0; ks < kBK / 16; ++ks) {
-        const int c = ks & 1, nx = c ^ 1;
-        constexpr int kLast = kBK / 16 - 1;
-        if (ks == kLast) {
-          // the next K-tile has landed and every wave is done reading this K-tile's stage
-          wait_vmem();
-          __syncthreads();
-        }
-        // this k-step's fragments, read by inline asm one k-step earlier
-        frag_wait<0>(ga[c], gb[c]);
-        const char *ra_ = ks < kLast ? sa : nxt;
-        const char *rb_ = ks < kLast ? sb : nxt + BM * 128;
-        const int ksn = ks < kLast ? ks + 1 : 0;
+              for (int j = 0; j < TN; ++j) {
+                tie(gb[c][j]);
+                if constexpr (BOP::kNeedsTail) gb[c][j] = BOP::mask(gb[c][j], BOP::frag_k0(kt, ks, ln), a.K);
+              }
+            }
+          } else if constexpr (ks == kLast) {
+            if constexpr (i == 0) {
+              // the next K-tile has landed and every wave is done reading this K-tile's stage
+              asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+              tie_all();
+              wait_vmem();
+              __syncthreads();
+            }
+          } else {
+            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(wcount(ks, i)));
+            tie(ga[ar]);
+            if constexpr (i == 0) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-#pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(ga[c][i], gb[c][j], acc[i][j]);
-#pragma unroll
-          for (int u = 0; u < kPerGroup1; ++u) {
-            const int q = (ks * TM + i) * kPerGroup1 + u;
-            if (q < PA)
-              opa.issue(ra, nxt, q, tp);
-            else if (q < PA + PB)
-              opb.issue(rb, nxt + BM * 128, q - PA, kn);
+              for (int j = 0; j < TN; ++j) tie(gb[c][j]);
+            }
           }
 #pragma unroll
-          for (int u = 0; u < kReadsPerGroup; ++u) {
-            const int slot = i * kReadsPerGroup + u;
-            if (slot < TN)
-              gb[nx][slot] = opb.frag(rb_, wave_n * WTN + slot * 32, ksn, lane);
-            else if (slot < TN + TM)
-              ga[nx][slot - TN] = opa.frag(ra_, wave_m * WTM + (slot - TN) * 32, ksn, lane);
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<DT>(ga[ar], gb[c][j], acc[i][j]);
+          if constexpr (!TAIL) {
+#pragma unroll
+            for (int u = 0; u < kPerGroup1; ++u) {
+              const int q = (ks * TM + i) * kPerGroup1 + u;
+              if (q < PA) {
+                if constexpr (AOP::kIsConv)
+                  opa.issue(ra, nxt, q, tp);
+                else
+                  opa.issue(ra, nxt, q, kn);
+              } else if (q < PA + PB) {
+                opb.issue(rb, nxt + BM * 128, q - PA, kn);
+              }
+            }
           }
+          if constexpr (!TAIL || ks < kLast) reads(k_c, i_c, TAIL ? sa : rs, ksn);
           __builtin_amdgcn_sched_barrier(0);
-        }
+        });
+      });
+    };
+
+    int kt = kt0;
+    for (;;) {
+      const int kstop = SERIAL ? min(split_end, kfull) : kfull;
+      for (; kt < kstop; ++kt) ktile1(kt, std::false_type{});
+      if constexpr (!SERIAL) {
+        break;
+      } else {
+        if (!at_boundary(kt)) break;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        tie_all();
+        park();
       }
     }
-    // the last prefetch (of a K-tile never computed) may still be in flight
-    frag_wait<0>(ga[0], gb[0]);
+    // the last prefetch (of the partial last K-tile, or of a K-tile never computed) may still be in
+    // flight
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    tie_all();
+    if constexpr (kAnyTail) {
+      // the partial last K-tile, already in LDS (loaded as a next K-tile by the loop, or by the
+      // prologue when it is the only one) with its first k-step's fragments read
+      if (tail_here) ktile1(kfull, std::true_type{});
+    }
   }
 
   // ---- epilogue. 32x32 accumulator layout: lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4,
@@ -715,13 +866,14 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     __syncthreads();  // every wave is done reading the last K-tile's fragments
     char *ct = smem + wave * (WTM * kRowB);
     const uint16_t *bias = (const uint16_t *)a.bias;
-    // SERIAL: the running sum of the earlier partitions, loaded one accumulator block ahead and
-    // added in front of the last partition's sum.
+    // SERIAL: the running sum of the earlier partitions (slot and LDS blocks loaded one accumulator
+    // block ahead, register blocks as they are), added in front of the last partition's sum.
     const bool has_slot = SERIAL && parked > 0;
     const uint32_t slot_lane = SERIAL ? slot_lane_at() : 0u;
     f32x4 ring[kSlotRing][4];
+    auto in_regs = [](int b) { return b >= kSlotBlocks && b < kSlotBlocks + kRegBlocks; };
     auto fetch = [&](int s, int i, int j) {
-      if (has_slot) {
+      if (has_slot && !in_regs(i + TM * j)) {
         if (kLdsBlocks > 0 && i == TM - 1 && j == TN - 1) {
           // the LDS-resident block (no loads in flight here: ordinary LDS reads)
           const char *lr = smem + 2 * kStage + wave * 4096 + lane_e * 16;
@@ -744,14 +896,17 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       const int cc = col_l + j * 32;
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        const int b = j * TM + i;  // fetch order
+        const int b = j * TM + i;  // block index (fetch order)
         float x[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) x[r] = acc[i][j][r];
         if constexpr (SERIAL) {
           constexpr int kAhead = kSlotRing - 1;
           if (b + kAhead < TM * TN) fetch((b + kAhead) % kSlotRing, (b + kAhead) % TM, (b + kAhead) / TM);
-          if (has_slot) {
+          if (has_slot && in_regs(b)) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) x[r] = run[b - kSlotBlocks][r] + x[r];
+          } else if (has_slot) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               const f32x4 v = ring[b % kSlotRing][q];

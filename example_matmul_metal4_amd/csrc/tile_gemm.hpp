@@ -42,6 +42,16 @@ __device__ __forceinline__ uint32_t lds_off(int row, int chunk) {
   return (uint32_t)(row * 128 + ((chunk ^ (row & 7) ^ ((row >> 3) & 7)) << 4));
 }
 
+// lds_off(rowblk + lane % 32, 2 * ks + lane / 32) for a row block rowblk that is a multiple of 32
+// (the 32x32x16 fragment a lane reads at k-step ks), written as a uniform part plus a per-lane part
+// that takes one of four values (k = 2 * ks ^ 4 * (rowblk / 32 % 2)) shared by every row block and
+// operand: the compiler keeps four lane offsets, not one per fragment.
+__device__ __forceinline__ uint32_t frag_off(int rowblk, int ks, int lane) {
+  const int k = (2 * ks) ^ (4 * ((rowblk >> 5) & 1));
+  const int t = (lane >> 5) ^ (lane & 7) ^ ((lane >> 3) & 3);
+  return (uint32_t)(rowblk * 128) + (uint32_t)((lane & 31) * 128 + ((k ^ t) << 4));
+}
+
 // Assemble a 16-byte chunk (8 halves) from 8/V loads of V halves each; off(g) gives the
 // byte offset of group g (out of range when masked).
 template <int V, typename OffFn>
