@@ -134,9 +134,13 @@ __device__ __forceinline__ void lds_direct16(rsrc_t r, char *lds, uint32_t off) 
 }
 
 // This lane's index in its wavefront, computed afresh (mbcnt), not derived from threadIdx: code
-// after a long loop that takes it from here holds nothing lane-specific across the loop.
+// after a long loop that takes it from here holds nothing lane-specific across the loop. Inline
+// asm, so that the compiler neither merges the calls into one value (which it then kept, and
+// spilled, across the loop) nor hoists them.
 __device__ __forceinline__ int lane_id() {
-  return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
 }
 
 // Wait until every vector-memory load of this wave has completed, direct-to-LDS ones included.

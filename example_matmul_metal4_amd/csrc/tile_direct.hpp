@@ -346,10 +346,13 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   // it in the slot, 191.0 with the LDS block, 176.4 with three register blocks as well and the
   // one-ahead loop; medians, one process, same bits).
   constexpr uint32_t kSlotBytes = BM * BN * 4;
-  // Slot traffic is streamed: sc1 (device scope: loads are served by L2, never by a possibly stale
-  // L1 line) + nt on stores and loads alike, which keeps it from displacing the A/B panels the
-  // other tiles of the XCD are reading (measured: 183 us vs 201 us with sc1 alone at config 2).
-  constexpr int kStorePolicy = 16 | 2;
+  // Slot traffic is streamed: nt on stores and loads alike, which keeps it from displacing the A/B
+  // panels the other tiles of the XCD are reading (measured: 183 us vs 201 us with sc1 alone at
+  // config 2), and sc1 on loads (device scope: served by L2, never by a possibly stale L1 line; a
+  // lane reads back only what it wrote itself, through the same XCD's L2). Stores without sc1
+  // measured 1.5-2 % faster with three register blocks (two sweeps of eight interleaved rounds;
+  // sc1 on loads only, sc0 or no policy on stores, sc1 alone: no faster).
+  constexpr int kStorePolicy = 2;
   constexpr int kLoadPolicy = 16 | 2;
   constexpr int kSlotRing = 2;  // accumulator blocks of the slot in flight (deeper rings spill)
   const rsrc_t rslot = make_rsrc(SERIAL ? a.partial + (size_t)t * (BM * BN) : nullptr, SERIAL ? kSlotBytes : 0u);
@@ -802,13 +805,17 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         park();
         const char *st = smem + ((kt - kt0) & 1) * kStage;
+        // the lane index taken afresh: addresses shared with the prologue's reads would otherwise
+        // be kept (and spilled) across the K loop
+        int ln = lane_id();
+        asm volatile("" : "+v"(ln));
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          gb[0][j] = opb.frag(st + BM * 128, wave_n * WTN + j * 32, 0, lane);
+          gb[0][j] = opb.frag(st + BM * 128, wave_n * WTN + j * 32, 0, ln);
           asm volatile("" : "=v"(gb[1][j]));  // a fresh value (overwritten before use)
         }
 #pragma unroll
-        for (int i = 0; i < TM; ++i) ga[i] = opa.frag(st, wave_m * WTM + i * 32, 0, lane);
+        for (int i = 0; i < TM; ++i) ga[i] = opa.frag(st, wave_m * WTM + i * 32, 0, ln);
         asm volatile("" : "=v"(ga[TM]));
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         tie_all();
