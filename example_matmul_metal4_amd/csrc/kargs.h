@@ -9,7 +9,13 @@
 
 #include <stdint.h>
 
-#define MTK_KARGS_VERSION 10
+#define MTK_KARGS_VERSION 11
+
+/* In-workgroup split-K: bytes of workspace slot per output tile of BM x BM (256 or 128). Each
+ * wavefront keeps these accumulator blocks (32 x 32 fp32, 4 KB) of its running sum in the slot,
+ * the others in registers and LDS: 256x256 tiles, 8 wavefronts x 4 blocks; 128x128 tiles,
+ * 4 wavefronts x 1 block. */
+#define MTK_SERIAL_SLOT_BYTES(BM) ((BM) == 256 ? 8 * 4 * 4096 : 4 * 1 * 4096)
 
 /* Tile-GEMM kernels: plain GEMM (A [M][K] . B, B either [N][K] or [K][N]) and
  * implicit-GEMM convolution (A = im2col of an NDHWC activation, B = DHWIO
@@ -20,8 +26,9 @@ typedef struct {
   const void *bias; /* [N] or NULL */
   void *C;          /* [M][ldc] output (f16/bf16), or NULL when writing partials */
   float *partial;   /* two-pass split-K: [split_k][M][N] fp32 partials (C NULL);
-                       in-workgroup split-K (*_s kernels): [tiles][BM*BN] running sums of
-                       the finished partitions (C set); else NULL */
+                       in-workgroup split-K (*_s kernels): [tiles][MTK_SERIAL_SLOT_BYTES(BM)]
+                       the part of each tile's running sum kept in the workspace (C set);
+                       else NULL */
   int32_t M, N, K;
   int32_t lda, ldb, ldc;
   uint32_t a_bytes, b_bytes; /* buffer-resource ranges: loads at or past these byte offsets return 0 */

@@ -408,7 +408,7 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
   set_args(g, a);
   p->launches.push_back(g);
   if (serial) {
-    p->workspace = (size_t)tiles * tile * tile * sizeof(float);  // one running-sum slot per tile
+    p->workspace = (size_t)tiles * MTK_SERIAL_SLOT_BYTES(tile);  // each tile's running-sum slot
   } else if (split > 1) {
     p->workspace = (size_t)split * d.M * d.N * sizeof(float);
     Launch r;

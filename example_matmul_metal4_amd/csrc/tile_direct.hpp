@@ -334,9 +334,10 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
 
   // SERIAL: the running sum of the finished partitions of this workgroup's tile lives in the
-  // tile's slot of the workspace ([tiles][BM*BN] fp32), in accumulator order (wave, block (i, j),
-  // register quad, lane): each lane moves 16 bytes per instruction, one instruction covers 1 KB of
-  // contiguous memory, and only this lane reads back what it wrote. The first boundary stores
+  // tile's slot of the workspace ([tiles][MTK_SERIAL_SLOT_BYTES(BM)]), in accumulator order (wave,
+  // block b = i + TM * j, register quad, lane): each lane moves 16 bytes per instruction, one
+  // instruction covers 1 KB of contiguous memory, and only this lane reads back what it wrote.
+  // Only the blocks b < kSlotBlocks live there (the others below). The first boundary stores
   // partition 0; later ones add the finished partition to the slot ((p0 + p1) + p2 ...); the
   // epilogue adds the slot in front of the last partition. Slot loads bypass L1 (device scope), so
   // a line read at one boundary is never served stale at the next. The last block (TM - 1, TN - 1)
@@ -345,7 +346,8 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   // 256x256 half of the running sum never leaves the CU (config 2 split-K 4: 196.7 us with all of
   // it in the slot, 191.0 with the LDS block, 176.4 with three register blocks as well and the
   // one-ahead loop; medians, one process, same bits).
-  constexpr uint32_t kSlotBytes = BM * BN * 4;
+  constexpr uint32_t kSlotBytes = NW * kSlotBlocks * 4096;
+  static_assert(!SERIAL || (BM == BN && kSlotBytes == MTK_SERIAL_SLOT_BYTES(BM)), "slot size shared with the host");
   // Slot traffic is streamed: nt on stores and loads alike, which keeps it from displacing the A/B
   // panels the other tiles of the XCD are reading (measured: 183 us vs 201 us with sc1 alone at
   // config 2), and sc1 on loads (device scope: served by L2, never by a possibly stale L1 line; a
@@ -355,7 +357,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   constexpr int kStorePolicy = 2;
   constexpr int kLoadPolicy = 16 | 2;
   constexpr int kSlotRing = 2;  // accumulator blocks of the slot in flight (deeper rings spill)
-  const rsrc_t rslot = make_rsrc(SERIAL ? a.partial + (size_t)t * (BM * BN) : nullptr, SERIAL ? kSlotBytes : 0u);
+  const rsrc_t rslot = make_rsrc(SERIAL ? a.partial + (size_t)t * (kSlotBytes / 4) : nullptr, SERIAL ? kSlotBytes : 0u);
   // LDS byte address of this lane's part of the LDS-resident running-sum block
   auto lds_run_at = [&]() {
     int l = lane_id();
@@ -366,7 +368,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   auto slot_lane_at = [&]() {
     int l = lane_id();
     asm volatile("" : "+v"(l));
-    return (uint32_t)(wave * (TM * TN * 1024) + l * 4) * 4u;
+    return (uint32_t)(wave * (kSlotBlocks * 1024) + l * 4) * 4u;
   };
   // Loads: the block's byte offset within the wave's part of the slot goes in the scalar offset
   // operand (it exceeds the 12-bit immediate): the lane part stays one register. Per-block lane
@@ -377,7 +379,7 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
   // VALU write of them in the very next instruction corrupted the stored data (measured: one such
   // instruction pair in a build of this kernel, that block's values non-repeatable in 31 of 256
   // tiles). With a constant scalar offset the compiler inserts the wait states itself.
-  auto slot_blk = [](int i, int j, int q) { return (i * TN + j) * 4096 + q * 1024; };
+  auto slot_blk = [](int i, int j, int q) { return (i + TM * j) * 4096 + q * 1024; };  // slot blocks only
   auto slot_load = [&](uint32_t slot_lane, int i, int j, int q) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rslot, slot_lane, slot_blk(i, j, q), kLoadPolicy));
   };

@@ -115,9 +115,10 @@ int mtk_set_stream(mtk_ctx *ctx, void *hip_stream);
  *                      then a second kernel sums them and adds the bias (the reference's
  *                      dispatch, matmul.swift:439-474);
  *   MTK_SPLIT_SERIAL   one workgroup per output tile runs the partitions in sequence, keeps the
- *                      running sum of the finished partitions in the workspace (one fp32 tile
- *                      per output tile) and adds it and the bias in its epilogue: no second
- *                      kernel (split_k <= 4).
+ *                      running sum of the finished partitions (part of it in the workspace: half
+ *                      an fp32 tile per 256x256 output tile, a quarter per 128x128 one; the rest
+ *                      on chip) and adds it and the bias in its epilogue: no second kernel
+ *                      (split_k <= 4).
  * k_stagger (split_k > 1): partition layout. Partition boundaries of output tile t sit at
  * s * ceil(k_tiles / split_k) + (t % S) - S / 2 K-tiles of 64 (0 < s < split_k), S the span:
  *   0 = the plan's choice (in-workgroup: up to 16, which spreads the tiles' partition ends over

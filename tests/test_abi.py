@@ -120,7 +120,8 @@ def test_gemm_kernel_select_dry():
     d = p.describe()
     assert d.endswith("kernels: mtk_gemm_f16_nt_256x256_s") and "split_k=4" in d and "grid=256 " in d
     assert "k_stagger=16 " in d
-    assert p.workspace_bytes == 256 * 256 * 256 * 4  # one running-sum slot per tile
+    # each tile's running-sum slot: half of the fp32 tile (four of each wavefront's eight blocks)
+    assert p.workspace_bytes == 256 * (256 * 256 * 4) // 2
     p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4, split_mode="two_pass")
     d = p.describe()
     assert d.endswith("kernels: mtk_gemm_f16_nt_256x256_d mtk_splitk_reduce_f16") and "grid=1024 " in d
@@ -139,7 +140,8 @@ def test_gemm_kernel_select_dry():
     # a small tile grid keeps the two-pass schedule (the partitions are the parallelism)
     assert "mtk_splitk_reduce_f16" in mtk.GemmPlan(None, 512, 512, 4100, split_k=4).describe()
     p = mtk.GemmPlan(None, 512, 512, 4100, split_k=4, split_mode="serial")
-    assert p.describe().endswith("kernels: mtk_gemm_f16_nt_128x128_s") and p.workspace_bytes == 16 * 128 * 128 * 4
+    # 128x128: one of each wavefront's four blocks in the slot
+    assert p.describe().endswith("kernels: mtk_gemm_f16_nt_128x128_s") and p.workspace_bytes == 16 * (128 * 128 * 4) // 4
     assert "_tn_256x256_s" in mtk.GemmPlan(None, 4096, 4096, 512, split_k=2, trans_a=True, trans_b=False,
                                             dtype="bf16").describe()
     p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4)
