@@ -91,6 +91,21 @@ __device__ __forceinline__ void wait_lds(u32x4 &f) { asm volatile("s_waitcnt lgk
 __device__ __forceinline__ void wait_lds2(u32x4 &f0, u32x4 &f1) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f0), "+v"(f1));
 }
+// lgkmcnt(N): all but the N youngest LDS reads done (they complete in issue order), tied to the
+// pair of fragments about to be used
+template <int N>
+__device__ __forceinline__ void wait_lds2_n(u32x4 &f0, u32x4 &f1) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(f0), "+v"(f1) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void wait_lds_n(u32x4 &f) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(f) : "i"(N));
+}
+// Fragment reads ahead of their MFMAs: a step pipeline of NS steps whose fragments are read R
+// steps ahead into a ring of R + 1 register sets (each step's reads are RPS LDS instructions).
+constexpr int ring_younger(int k, int ns, int r, int rps) { return rps * (k + r < ns ? r : ns - 1 - k); }
 
 // Park a wavefront's 16 x 256 accumulator tile (lane: rows 4 (l / 16) + e, column 16 db + l % 16)
 // in LDS as 512-byte rows and store chunks below nchunk of rows below rows_valid, 16 bytes per
@@ -193,18 +208,39 @@ __device__ __forceinline__ void dkdv(const mtk_attn_bwd_kargs &a) {
     if (i + 1 < n_steps) stage((i + 1) & 1, i + 1);
     const char *qt = smem + (i & 1) * 2 * kTileB, *gt = qt + kTileB;
 
-    // S^T = K.Q^T and dP^T = V.dO^T for the tile's two blocks of 16 queries
+    // S^T = K.Q^T and dP^T = V.dO^T for the tile's two blocks of 16 queries: 16 steps (d-step st,
+    // query block nb inner, so four accumulator chains alternate), fragments read kR1 steps ahead
     f32x4 s[2] = {f32x4{}, f32x4{}}, p[2] = {f32x4{}, f32x4{}};
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        u32x4 fq = rd128(row_frag_addr(qt, 16 * nb, st, lane));
-        u32x4 fg = rd128(row_frag_addr(gt, 16 * nb, st, lane));
-        wait_lds2(fq, fg);
-        s[nb] = mfma16x16x32<DT>(kf[st], fq, s[nb]);
-        p[nb] = mfma16x16x32<DT>(vf[st], fg, p[nb]);
+    {
+      constexpr int kNS = 16, kR1 = 4;
+      u32x4 fr[kR1 + 1][2];
+      auto rd = [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (k < kNS) {
+          fr[k % (kR1 + 1)][0] = rd128(row_frag_addr(qt, 16 * (k % 2), k / 2, lane));
+          fr[k % (kR1 + 1)][1] = rd128(row_frag_addr(gt, 16 * (k % 2), k / 2, lane));
+        }
+      };
+      static_for<0, kR1>(rd);
+      static_for<0, kNS>([&](auto kc) {
+        constexpr int k = decltype(kc)::value, st = k / 2, nb = k % 2;
+        rd(std::integral_constant<int, k + kR1>{});
+        wait_lds2_n<ring_younger(k, kNS, kR1, 2)>(fr[k % (kR1 + 1)][0], fr[k % (kR1 + 1)][1]);
+        s[nb] = mfma16x16x32<DT>(kf[st], fr[k % (kR1 + 1)][0], s[nb]);
+        p[nb] = mfma16x16x32<DT>(vf[st], fr[k % (kR1 + 1)][1], p[nb]);
+      });
+    }
+    // dV / dK fragments: the first kR2 steps' transposed reads go out before the softmax work
+    constexpr int kNS2 = 16, kR2 = 3;
+    u32x4 fr2[kR2 + 1][2];
+    auto rd2 = [&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      if constexpr (k < kNS2) {
+        fr2[k % (kR2 + 1)][0] = rd_tr(tr_addr(gt, k, 0, lane), tr_addr(gt, k, 1, lane));
+        fr2[k % (kR2 + 1)][1] = rd_tr(tr_addr(qt, k, 0, lane), tr_addr(qt, k, 1, lane));
       }
+    };
+    static_for<0, kR2>(rd2);
     // P^T = exp2(S^T scale log2e - lse2) and dS^T = P^T (dP^T scale - D scale), masked, rounded to
     // the input type into the scratch ([16 keys][32 queries])
 #pragma unroll
@@ -222,19 +258,20 @@ __device__ __forceinline__ void dkdv(const mtk_attn_bwd_kargs &a) {
         wr16(scr_s + o, to_bits<DT>(sv));
       }
     }
-    // A operands: key l % 16, queries 8 (l / 16) .. + 7 (the same wavefront's writes above come first)
+    // A operands: key l % 16, queries 8 (l / 16) .. + 7 (the same wavefront's writes above come first;
+    // the wait also covers the transposed reads issued before them)
     u32x4 pa = rd128(scr_p + (uint32_t)(l16 * kScrRow + 16 * g));
     u32x4 sa = rd128(scr_s + (uint32_t)(l16 * kScrRow + 16 * g));
     wait_lds2(pa, sa);
-    // dV += P^T.dO and dK += dS^T.Q, 16 blocks of 16 dims each
-#pragma unroll
-    for (int db = 0; db < 16; ++db) {
-      u32x4 bg = rd_tr(tr_addr(gt, db, 0, lane), tr_addr(gt, db, 1, lane));
-      u32x4 bq = rd_tr(tr_addr(qt, db, 0, lane), tr_addr(qt, db, 1, lane));
-      wait_lds2(bg, bq);
-      dv[db] = mfma16x16x32<DT>(pa, bg, dv[db]);
-      dk[db] = mfma16x16x32<DT>(sa, bq, dk[db]);
-    }
+    // dV += P^T.dO and dK += dS^T.Q, 16 blocks of 16 dims each, fragments kR2 steps ahead (four
+    // transposed reads per step)
+    static_for<0, kNS2>([&](auto kc) {
+      constexpr int db = decltype(kc)::value;
+      rd2(std::integral_constant<int, db + kR2>{});
+      wait_lds2_n<ring_younger(db, kNS2, kR2, 4)>(fr2[db % (kR2 + 1)][0], fr2[db % (kR2 + 1)][1]);
+      dv[db] = mfma16x16x32<DT>(pa, fr2[db % (kR2 + 1)][0], dv[db]);
+      dk[db] = mfma16x16x32<DT>(sa, fr2[db % (kR2 + 1)][1], dk[db]);
+    });
   }
 
   wait_vmem();
@@ -246,7 +283,10 @@ __device__ __forceinline__ void dkdv(const mtk_attn_bwd_kargs &a) {
   store_tile<DT>(park + 16 * kRowB, dv, (uint16_t *)a.dV + e0, ld, a.S_kv - k0, nchunk, lane);
 }
 
-template <int DT, bool CAUSAL>
+// Read-ahead depths of dQ's two step pipelines: the deepest that keep two wavefronts per SIMD
+// (deeper rings measured slower at one: 2,663 against 2,085 us at the config 5 shape, D = 256;
+// the causal kernel's masks take the registers of one more step)
+template <int DT, bool CAUSAL, int kDqAhead1 = CAUSAL ? 1 : 2, int kDqAhead2 = 2>
 __device__ __forceinline__ void dq(const mtk_attn_bwd_kargs &a) {
   // two slots of (K tile, V tile), then the wavefronts' dS scratch
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTileB + 4 * kScrB];
@@ -320,18 +360,36 @@ __device__ __forceinline__ void dq(const mtk_attn_bwd_kargs &a) {
     if (t + 1 < n_tiles) stage((t + 1) & 1, t + 1);
     const char *kt = smem + (t & 1) * 2 * kTileB, *vt = kt + kTileB;
 
-    // S = Q.K^T and dP = dO.V^T for the tile's two blocks of 16 keys
+    // S = Q.K^T and dP = dO.V^T for the tile's two blocks of 16 keys (the same step pipeline as the
+    // dK/dV kernel's)
     f32x4 s[2] = {f32x4{}, f32x4{}}, p[2] = {f32x4{}, f32x4{}};
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        u32x4 fk = rd128(row_frag_addr(kt, 16 * nb, st, lane));
-        u32x4 fv = rd128(row_frag_addr(vt, 16 * nb, st, lane));
-        wait_lds2(fk, fv);
-        s[nb] = mfma16x16x32<DT>(qf[st], fk, s[nb]);
-        p[nb] = mfma16x16x32<DT>(gf[st], fv, p[nb]);
-      }
+    {
+      constexpr int kNS = 16, kR1 = kDqAhead1;
+      u32x4 fr[kR1 + 1][2];
+      auto rd = [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (k < kNS) {
+          fr[k % (kR1 + 1)][0] = rd128(row_frag_addr(kt, 16 * (k % 2), k / 2, lane));
+          fr[k % (kR1 + 1)][1] = rd128(row_frag_addr(vt, 16 * (k % 2), k / 2, lane));
+        }
+      };
+      static_for<0, kR1>(rd);
+      static_for<0, kNS>([&](auto kc) {
+        constexpr int k = decltype(kc)::value, st = k / 2, nb = k % 2;
+        rd(std::integral_constant<int, k + kR1>{});
+        wait_lds2_n<ring_younger(k, kNS, kR1, 2)>(fr[k % (kR1 + 1)][0], fr[k % (kR1 + 1)][1]);
+        s[nb] = mfma16x16x32<DT>(qf[st], fr[k % (kR1 + 1)][0], s[nb]);
+        p[nb] = mfma16x16x32<DT>(gf[st], fr[k % (kR1 + 1)][1], p[nb]);
+      });
+    }
+    // dQ fragments: the first kR2 steps' transposed reads go out before the softmax work
+    constexpr int kNS2 = 16, kR2 = kDqAhead2;
+    u32x4 fr2[kR2 + 1];
+    auto rd2 = [&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      if constexpr (k < kNS2) fr2[k % (kR2 + 1)] = rd_tr(tr_addr(kt, k, 0, lane), tr_addr(kt, k, 1, lane));
+    };
+    static_for<0, kR2>(rd2);
     // dS = P (dP scale - D scale), P = exp2(S scale log2e - lse2), masked, into the scratch
     // ([16 queries][32 keys])
 #pragma unroll
@@ -348,13 +406,13 @@ __device__ __forceinline__ void dq(const mtk_attn_bwd_kargs &a) {
     }
     u32x4 sa = rd128(scr + (uint32_t)(l16 * kScrRow + 16 * g));
     wait_lds(sa);
-    // dQ += dS.K, 16 blocks of 16 dims
-#pragma unroll
-    for (int db = 0; db < 16; ++db) {
-      u32x4 bk = rd_tr(tr_addr(kt, db, 0, lane), tr_addr(kt, db, 1, lane));
-      wait_lds(bk);
-      acc[db] = mfma16x16x32<DT>(sa, bk, acc[db]);
-    }
+    // dQ += dS.K, 16 blocks of 16 dims, fragments kR2 steps ahead (two transposed reads per step)
+    static_for<0, kNS2>([&](auto kc) {
+      constexpr int db = decltype(kc)::value;
+      rd2(std::integral_constant<int, db + kR2>{});
+      wait_lds_n<ring_younger(db, kNS2, kR2, 2)>(fr2[db % (kR2 + 1)]);
+      acc[db] = mfma16x16x32<DT>(sa, fr2[db % (kR2 + 1)], acc[db]);
+    });
   }
 
   wait_vmem();
