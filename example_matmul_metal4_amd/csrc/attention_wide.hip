@@ -59,6 +59,15 @@ __device__ __forceinline__ void wr16(uint32_t addr, uint32_t v) {
   asm volatile("ds_write_b16 %0, %1" ::"v"(addr), "v"(v) : "memory");
 }
 __device__ __forceinline__ void wait_lds(u32x4 &f) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f)); }
+// lgkmcnt(N): all but the N youngest LDS reads done (they complete in issue order), tied to the
+// fragment about to be used
+template <int N>
+__device__ __forceinline__ void wait_lds_n(u32x4 &f) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(f) : "i"(N));
+}
+// reads issued after step k's in a pipeline of ns steps read r steps ahead, rps reads per step
+constexpr int ring_younger(int k, int ns, int r, int rps) { return rps * (k + r < ns ? r : ns - 1 - k); }
 
 // max / sum over the 16 lanes that share l / 16 (the keys of one query row)
 __device__ __forceinline__ float row16_max(float x) {
@@ -109,7 +118,9 @@ __device__ __forceinline__ void fwd(const mtk_attn_kargs &a) {
     qf[s] = buf_load16(rq, off);
   }
   // accumulator rows of this lane: queries q0 + 4 (l / 16) + e; running max (base 2) and this
-  // lane's part of the row sums (its keys l % 16 and 16 + l % 16 of every tile)
+  // lane's part of the row sums (its keys l % 16 and 16 + l % 16 of every tile). (The 128-query
+  // kernel's lazy rescale, O rescaled only when the max moves by more than 8, spilled here: the
+  // branch around the 128 accumulator registers' rescale took 200 bytes per lane of scratch.)
   f32x4 o[kDBlocks];
 #pragma unroll
   for (int i = 0; i < kDBlocks; ++i) o[i] = f32x4{};
@@ -138,20 +149,43 @@ __device__ __forceinline__ void fwd(const mtk_attn_kargs &a) {
     if (t + 1 < n_tiles) stage((t + 1) & 1, t + 1);
     const char *kt = smem + (t & 1) * 2 * kTileB, *vt = kt + kTileB;
 
-    // S = Q.K^T for the tile's two blocks of 16 keys
-    // (fragments read four at a time, then one wait)
+    // S = Q.K^T for the tile's two blocks of 16 keys: 2 kSteps steps (d-step outer, key block inner,
+    // so the two accumulator chains alternate), K fragments read kR1 steps ahead through a ring
     f32x4 s[2] = {f32x4{}, f32x4{}};
+    {
+      constexpr int kNS = 2 * kSteps, kR1 = 8;
+      u32x4 fr[kR1 + 1];
+      auto rd = [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr (k < kNS) fr[k % (kR1 + 1)] = rd128(lds_addr(kt) + chunk_off(16 * (k % 2) + l16, 4 * (k / 2) + g));
+      };
+      static_for<0, kR1>(rd);
+      static_for<0, kNS>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        rd(std::integral_constant<int, k + kR1>{});
+        wait_lds_n<ring_younger(k, kNS, kR1, 1)>(fr[k % (kR1 + 1)]);
+        s[k % 2] = mfma16x16x32<DT>(qf[k / 2], fr[k % (kR1 + 1)], s[k % 2]);
+      });
+    }
+    // V^T fragments of the P.V product (keys 8 (l / 16) .. + 7 of dim 16 db + l % 16), read kR2
+    // steps ahead; the first kR2 go out before the softmax work
+    constexpr int kR2 = 6;
+    u32x4 fv[kR2 + 1];
+    auto rdv = [&](auto kc) {
+      constexpr int db = decltype(kc)::value;
+      if constexpr (db < kDBlocks) {
+        const int sl = lane & 15;
+        uint32_t ad[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int s4 = 0; s4 < kSteps; s4 += 4) {
-        u32x4 fk[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) fk[u] = rd128(lds_addr(kt) + chunk_off(16 * nb + l16, 4 * (s4 + u) + g));
-        lgkm_wait0(fk);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) s[nb] = mfma16x16x32<DT>(qf[s4 + u], fk[u], s[nb]);
+        for (int hf = 0; hf < 2; ++hf) {
+          const int row = 8 * g + 4 * hf + (sl >> 2);
+          const int d = 16 * db + 4 * (sl & 3);
+          ad[hf] = lds_addr(vt) + (uint32_t)(row * kRowB + (((d >> 3) ^ swz(row)) << 4) + 2 * (d & 7));
+        }
+        fv[db % (kR2 + 1)] = rd_tr(ad[0], ad[1]);
       }
+    };
+    static_for<0, kR2>(rdv);
     // online softmax in base 2: x = S scale log2(e), masked to -inf past S_kv or the diagonal
     float x[2][4], mt[4];
 #pragma unroll
@@ -181,29 +215,17 @@ __device__ __forceinline__ void fwd(const mtk_attn_kargs &a) {
         wr16(scr + (uint32_t)((4 * g + e) * kScrRow + (16 * nb + l16) * 2), to_bits<DT>(p));
       }
     }
-    // P as the A operand: query l % 16, keys 8 (l / 16) .. + 7 (this wavefront's writes come first)
+    // P as the A operand: query l % 16, keys 8 (l / 16) .. + 7 (this wavefront's writes come first;
+    // the wait also covers the V^T reads issued before them)
     u32x4 pa = rd128(scr + (uint32_t)(l16 * kScrRow + 16 * g));
     wait_lds(pa);
-    // O += P.V, one MFMA per 16-dim block; V^T fragments: keys 8 (l / 16) .. + 7 of dim 16 db + l % 16
-#pragma unroll
-    for (int d4 = 0; d4 < kDBlocks; d4 += 4) {
-      u32x4 bv[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int sl = lane & 15;
-        uint32_t ad[2];
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int row = 8 * g + 4 * hf + (sl >> 2);
-          const int d = 16 * (d4 + u) + 4 * (sl & 3);
-          ad[hf] = lds_addr(vt) + (uint32_t)(row * kRowB + (((d >> 3) ^ swz(row)) << 4) + 2 * (d & 7));
-        }
-        bv[u] = rd_tr(ad[0], ad[1]);
-      }
-      lgkm_wait0(bv);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) o[d4 + u] = mfma16x16x32<DT>(pa, bv[u], o[d4 + u]);
-    }
+    // O += P.V, one MFMA per 16-dim block (two transposed reads per step)
+    static_for<0, kDBlocks>([&](auto kc) {
+      constexpr int db = decltype(kc)::value;
+      rdv(std::integral_constant<int, db + kR2>{});
+      wait_lds_n<ring_younger(db, kDBlocks, kR2, 2)>(fv[db % (kR2 + 1)]);
+      o[db] = mfma16x16x32<DT>(pa, fv[db % (kR2 + 1)], o[db]);
+    });
   }
 
   // O / l; lse = (m + log2 l) ln 2 (natural log), -inf for a row that sees no key (O = 0)
