@@ -1,6 +1,6 @@
 // Flash-attention forward for gfx950, head dimension 128: the 128-query kernel (attention.hpp,
-// padded head dimension 128) and the ping-pong kernel below, which is specific to D = 128.
-// Other head dimensions are instantiated in attention_hd.hip.
+// padded head dimension 128) and the ping-pong kernel below, compiled for D = 128 and D = 64
+// exactly. Other head dimensions are instantiated in attention_hd.hip.
 //
 // Two kernels share the arithmetic at D = 128 (their outputs are equal bit for bit): attn_fwd, 4
 // wavefronts x 32 queries with the MFMA and softmax work of consecutive tiles interleaved in each
@@ -11,8 +11,6 @@
 
 namespace mtk {
 
-constexpr int kD = 128;
-constexpr int kTile = AttnLayout<kD>::kTile;  // bytes of one K or V tile in LDS
 
 // ---------------------------------------------------------------------------------------------
 // Ping-pong variant: 8 wavefronts (two per SIMD) per workgroup, 256 queries, 32 per wavefront, one
@@ -27,8 +25,14 @@ constexpr int kTile = AttnLayout<kD>::kTile;  // bytes of one K or V tile in LDS
 // 2k+1) and waited for before barrier 2k+3. Same arithmetic as attn_fwd (attention.hpp) at D = 128.
 constexpr int kBQP = 256;
 
-template <int DT, bool CAUSAL>
+// DP: the head dimension (128, or 64: the same schedule with half the k-steps and d blocks, rows of
+// 128 bytes in LDS with the 128-query kernel's swizzles for that width).
+template <int DT, bool CAUSAL, int DP = 128>
 __device__ __forceinline__ void attn_fwd_pp(const mtk_attn_kargs &a) {
+  using L = AttnLayout<DP>;
+  static_assert(DP == 128 || DP == 64, "ping-pong head dimension");
+  constexpr int kD = DP, kTile = L::kTile, kRowB = L::kRowB, kKs = L::kKs, kDb = L::kDb;
+  constexpr int kNiW = kTile / 1024 / 8;  // staging instructions per wavefront and tile
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTile];  // K slots 0, 1 then V slots 0, 1
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -57,70 +61,78 @@ __device__ __forceinline__ void attn_fwd_pp(const mtk_attn_kargs &a) {
 
   const int wave_q_min = q0 + wave * 32;
   const int qi = wave_q_min + col;
-  u32x4 qf[8];
+  u32x4 qf[kKs];
 #pragma unroll
-  for (int ds = 0; ds < 8; ++ds)
+  for (int ds = 0; ds < kKs; ++ds)
     qf[ds] = buf_load16(rq, qi < a.S_q ? qbase + (uint32_t)qi * rs + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB);
 
   int kv_end = a.S_kv;
   if (CAUSAL) kv_end = min(a.S_kv, q0 + kBQP + diag);
   const int n_tiles = kv_end > 0 ? (kv_end + kBKV - 1) / kBKV : 0;
 
-  // direct-to-LDS staging: each wavefront fills 2 KB of a tile (two instructions of 4 rows). K:
-  // LDS chunk pc of row r holds global chunk pc ^ (r & 15); V: pc ^ 4 * (r & 3). Only the in-range
-  // offsets are kept in registers; the row-checked path of the tile crossing S_kv recomputes them.
-  auto stage_row = [&](int i) { return (wave * 2 + i) * 4 + (lane >> 4); };
+  // direct-to-LDS staging: each wavefront fills an eighth of a tile (D = 128: two instructions of
+  // 4 rows; D = 64: one of 8 rows). LDS chunk pc of row r holds global chunk pc ^ kswz(r) (K) or
+  // pc ^ vswz(r) (V) (D = 128: r & 15 and 4 (r & 3)). Only the in-range offsets are kept in
+  // registers; the row-checked path of the tile crossing S_kv recomputes them.
+  auto stage_row = [&](int i) { return (wave * kNiW + i) * L::kRpi + lane / L::kCpr; };
   auto stage_col = [&](int i, bool is_k) {
-    const int r = stage_row(i), pc = lane & 15;
-    return 16u * (uint32_t)(is_k ? (pc ^ (r & 15)) : (pc ^ (4 * (r & 3))));
+    const int r = stage_row(i), pc = lane % L::kCpr;
+    return 16u * (uint32_t)(is_k ? (pc ^ L::kswz(r)) : (pc ^ L::vswz(r)));
   };
-  uint32_t klane[2], vlane[2];
+  uint32_t klane[kNiW], vlane[kNiW];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < kNiW; ++i) {
     klane[i] = (uint32_t)stage_row(i) * rkv + stage_col(i, true);
     vlane[i] = (uint32_t)stage_row(i) * rkv + stage_col(i, false);
   }
-  auto issue = [&](const rsrc_t &r, char *dst, const uint32_t (&lane_off)[2], bool is_k, int t) {
+  auto issue = [&](const rsrc_t &r, char *dst, const uint32_t (&lane_off)[kNiW], bool is_k, int t) {
     const int key0 = t * kBKV;
     if (key0 + kBKV <= a.S_kv) {
       const uint32_t tb = kvbase + (uint32_t)key0 * rkv;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) lds_direct16_s(r, dst + i * 1024, lane_off[i], tb);
+      for (int i = 0; i < kNiW; ++i) lds_direct16_s(r, dst + i * 1024, lane_off[i], tb);
     } else {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < kNiW; ++i) {
         const int key = key0 + stage_row(i);
         lds_direct16(r, dst + i * 1024, key < a.S_kv ? kvbase + (uint32_t)key * rkv + stage_col(i, is_k) : kOOB);
       }
     }
   };
-  auto issue_k = [&](int t) { issue(rk, smem + (t & 1) * kTile + wave * 2048, klane, true, t); };
-  auto issue_v = [&](int t) { issue(rv, smem + (2 + (t & 1)) * kTile + wave * 2048, vlane, false, t); };
+  auto issue_k = [&](int t) { issue(rk, smem + (t & 1) * kTile + wave * (kTile / 8), klane, true, t); };
+  auto issue_v = [&](int t) { issue(rv, smem + (2 + (t & 1)) * kTile + wave * (kTile / 8), vlane, false, t); };
 
   // Fragment addresses from one base per lane: K k-step ds is at chunk (2 ds + g) ^ (krow & 15) =
   // 2 (ds ^ zh) + ((g ^ krow) & 1) with zh = (krow & 15) >> 1; V^T d block db at chunk
-  // (4 db + x) ^ 4 y = 4 (db ^ y) + x (see vread for x, y). Fewer live registers than a table.
+  // (4 db + x) ^ 4 y = 4 (db ^ y) + x (x, y: the V^T read's chunk and row parts). Fewer live registers
+  // than a table.
+  // (D = 64: the same chunks from the 128-byte rows' swizzles, k-step ds and d block db folded into
+  // the per-lane offset.)
   const int krow = swap_bits_2_3(col);
   const uint32_t kbase0 = (uint32_t)(krow * 256 + 16 * ((g ^ krow) & 1));
   const int kzh = (krow & 15) >> 1;
-  auto kq = [&](int ds) { return kbase0 + 32u * (uint32_t)(ds ^ kzh); };
+  auto kq = [&](int ds) {
+    if constexpr (DP == 128)
+      return kbase0 + 32u * (uint32_t)(ds ^ kzh);
+    else
+      return (uint32_t)(krow * kRowB + (((2 * ds + g) ^ L::kswz(krow)) << 4));
+  };
   const int vs = lane & 15, vh = lane >> 4;
   const int vrow = 8 * (vh >> 1) + (vs >> 2), vy = vrow & 3;
   const uint32_t vbase0 = lds_addr(smem) + (uint32_t)(vrow * 256 + 16 * (2 * (vh & 1) + ((vs & 3) >> 1)) + 2 * (4 * (vs & 3) & 7));
-  auto vq = [&](int db) { return vbase0 + 64u * (uint32_t)(db ^ vy); };
-  auto vread = [&](u32x4 (&dst)[4], uint32_t vb) {
-    static_for<0, 4>([&](auto jc) {
-      constexpr int JS = decltype(jc)::value;
-      const u32x2 w0 = ds_read_tr16_at<4096 * JS>(vb);
-      const u32x2 w1 = ds_read_tr16_at<4096 * JS + 1024>(vb);
-      dst[JS] = u32x4{w0.x, w0.y, w1.x, w1.y};
-    });
+  auto vq = [&](int db) {
+    if constexpr (DP == 128) {
+      return vbase0 + 64u * (uint32_t)(db ^ vy);
+    } else {
+      const int d = 32 * db + 16 * (vh & 1) + 4 * (vs & 3);
+      return lds_addr(smem) + (uint32_t)(vrow * kRowB + 16 * ((d >> 3) ^ L::vswz(vrow)) + 2 * (d & 7));
+    }
   };
 
   float m_off = -INFINITY, l_run = 0.0f;
-  f32x16 o[4];
+  f32x16 o[kDb];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
+  for (int i = 0; i < kDb; ++i) o[i] = f32x16{};
   f32x16 s0 = f32x16{}, s1 = f32x16{};  // S^T of the latest tile
   u32x4 pf[4];                          // P of the latest softmaxed tile
 #pragma unroll
@@ -137,7 +149,7 @@ __device__ __forceinline__ void attn_fwd_pp(const mtk_attn_kargs &a) {
   constexpr int kLook = 6, kRing = kLook + 2;
   auto mfma_block = [&](int k, auto pv_c, auto sk_c) {
     constexpr bool PV = decltype(pv_c)::value, SK = decltype(sk_c)::value;
-    constexpr int kPerDb = (SK ? 2 : 0) + (PV ? 4 : 0), kSteps = 4 * kPerDb;
+    constexpr int kPerDb = (SK ? 2 : 0) + (PV ? 4 : 0), kSteps = kDb * kPerDb;
     const uint32_t vt = (uint32_t)((2 + ((k - 1) & 1)) * kTile);
     const uint32_t kslot = lds_addr(smem) + (uint32_t)((k & 1) * kTile);
     u32x4 ring[kRing][2];
@@ -147,12 +159,12 @@ __device__ __forceinline__ void attn_fwd_pp(const mtk_attn_kargs &a) {
       if constexpr (IS_S) {
         const uint32_t ka = kslot + kq(2 * DB + W);
         ring[S % kRing][0] = ds_read_b128_at<0>(ka);
-        ring[S % kRing][1] = ds_read_b128_at<8192>(ka);
+        ring[S % kRing][1] = ds_read_b128_at<32 * kRowB>(ka);  // key block 1: 32 rows on
       } else {
         constexpr int JS = W - (SK ? 2 : 0);
         const uint32_t vb = vq(DB) + vt;
-        const u32x2 w0 = ds_read_tr16_at<4096 * JS>(vb);
-        const u32x2 w1 = ds_read_tr16_at<4096 * JS + 1024>(vb);
+        const u32x2 w0 = ds_read_tr16_at<16 * kRowB * JS>(vb);
+        const u32x2 w1 = ds_read_tr16_at<16 * kRowB * JS + 4 * kRowB>(vb);
         ring[S % kRing][0] = u32x4{w0.x, w0.y, w1.x, w1.y};
       }
     };
@@ -205,7 +217,7 @@ __device__ __forceinline__ void attn_fwd_pp(const mtk_attn_kargs &a) {
     if (__any(alpha != 1.0f)) {
       // one accumulator block at a time: at most 16 values in flight through temporaries
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kDb; ++i) {
         o[i] *= alpha;
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -282,7 +294,7 @@ __device__ __forceinline__ void attn_fwd_pp(const mtk_attn_kargs &a) {
     uint16_t *O = (uint16_t *)a.O;
     const size_t obase = (((size_t)b * a.S_q + qi) * a.H + h) * kD;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < kDb; ++db)
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const int d = db * 32 + 8 * rq + 4 * g;
@@ -302,13 +314,17 @@ MTK_ATTN_FWD_KERNEL(mtk_attn_fwd_bf16, DT_BF16, false, 128, false, 2)
 MTK_ATTN_FWD_KERNEL(mtk_attn_fwd_f16_causal, DT_F16, true, 128, false, 2)
 MTK_ATTN_FWD_KERNEL(mtk_attn_fwd_bf16_causal, DT_BF16, true, 128, false, 2)
 
-#define ATTN_PP_KERNEL(NAME, DT, CAUSAL)                                                               \
+#define ATTN_PP_KERNEL(NAME, DT, CAUSAL, DP)                                                           \
   extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))        \
   NAME(const mtk_attn_kargs a) {                                                                       \
-    attn_fwd_pp<DT, CAUSAL>(a);                                                                        \
+    attn_fwd_pp<DT, CAUSAL, DP>(a);                                                                    \
   }
 
-ATTN_PP_KERNEL(mtk_attn_fwd_pp_f16, DT_F16, false)
-ATTN_PP_KERNEL(mtk_attn_fwd_pp_bf16, DT_BF16, false)
-ATTN_PP_KERNEL(mtk_attn_fwd_pp_f16_causal, DT_F16, true)
-ATTN_PP_KERNEL(mtk_attn_fwd_pp_bf16_causal, DT_BF16, true)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_f16, DT_F16, false, 128)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_bf16, DT_BF16, false, 128)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_f16_causal, DT_F16, true, 128)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_bf16_causal, DT_BF16, true, 128)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_d64_f16, DT_F16, false, 64)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_d64_bf16, DT_BF16, false, 64)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_d64_f16_causal, DT_F16, true, 64)
+ATTN_PP_KERNEL(mtk_attn_fwd_pp_d64_bf16_causal, DT_BF16, true, 64)

@@ -755,8 +755,8 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "attention dtype must be MTK_F16 or MTK_BF16");
   if (d.q_rows != 0 && d.q_rows != 128 && d.q_rows != 256)
     return fail(MTK_ERR_INVALID, "q_rows must be 0, 128 or 256 (got %d)", d.q_rows);
-  if (d.q_rows == 256 && d.D != 128)
-    return fail(MTK_ERR_UNSUPPORTED, "q_rows 256 (the ping-pong kernel) needs head dimension 128 (got %d)", d.D);
+  if (d.q_rows == 256 && d.D != 128 && d.D != 64)
+    return fail(MTK_ERR_UNSUPPORTED, "q_rows 256 (the ping-pong kernel) needs head dimension 128 or 64 (got %d)", d.D);
   const uint64_t q_bytes = (uint64_t)d.B * d.S_q * d.H * d.D * 2;
   const uint64_t kv_bytes = (uint64_t)d.B * d.S_kv * d.H_kv * d.D * 2;
   if (q_bytes > kMaxOperandBytes || kv_bytes > kMaxOperandBytes)
@@ -772,19 +772,22 @@ int plan_attn(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   const bool gen = d.D % 8 != 0;
   p->align_a = p->align_b = gen ? 2 : 16;
   // Query rows per workgroup: 256 (the ping-pong kernel: 8 wavefronts in two groups alternating MFMA
-  // and softmax blocks, one workgroup per CU) for non-causal D = 128 grids that still fill the device
-  // (config 5, one box: 526.5 us against 546.5 us for 128 rows); 128 (4 wavefronts, two workgroups
+  // and softmax blocks, one workgroup per CU) for non-causal D = 128 and D = 64 grids that still fill
+  // the device (config 5, one box: 526.5 us against 546.5 us for 128 rows; at D = 64 368.8 against
+  // 412.4 us); 128 (4 wavefronts, two workgroups
   // per CU) otherwise, causal included (config 5 causal, one box: 298.7 us against 305.3 us for the
   // ping-pong kernel, both in the kernels' balanced causal dispatch order).
   int rows = d.q_rows;
   if (rows == 0) {
     const int cus = ctx ? ctx->prop.multiProcessorCount : 256;
-    rows = (d.D == 128 && !d.causal && (long long)d.B * d.H * ((d.S_q + 255) / 256) >= cus) ? 256 : 128;
+    rows = ((d.D == 128 || d.D == 64) && !d.causal && (long long)d.B * d.H * ((d.S_q + 255) / 256) >= cus) ? 256 : 128;
     if (wide) rows = 64;
   }
   Launch g;
-  std::string family = rows == 256 ? "pp_" : "";
-  if (gen)
+  std::string family;
+  if (rows == 256)
+    family = dp == 128 ? "pp_" : "pp_d64_";  // D = 128 or 64 exactly
+  else if (gen)
     family = "g" + std::to_string(dp) + "_";
   else if (dp != 128)
     family = "d" + std::to_string(dp) + "_";

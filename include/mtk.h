@@ -188,7 +188,7 @@ int mtk_gemm_run_noalloc(const mtk_plan *plan, const mtk_gemm_args *args);
  * causal != 0 keeps keys j <= i + (S_kv - S_q) for query i (bottom-right aligned).
  * q_rows: query rows per workgroup, 0 = let the plan choose; 128 (4 wavefronts of 32 queries, two
  * workgroups per CU) or 256 (8 wavefronts of 32 queries in two groups that alternate MFMA and
- * softmax blocks, one workgroup per CU; D = 128 only). Same results bit for bit. */
+ * softmax blocks, one workgroup per CU; D = 128 or 64 only). Same results bit for bit. */
 #define MTK_ATTN_MAX_HEAD_DIM 512
 
 typedef struct {

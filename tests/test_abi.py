@@ -297,8 +297,14 @@ def test_attention_select_and_validation():
         assert p.describe().endswith(f"kernels: mtk_attn_fwd_{fam}f16"), (D, p.describe())
         assert p.work()[0] == 4 * 2 * D * 300 * 300
     assert mtk.AttentionPlan(None, 2, 32, 4096, 4096, 64, causal=True).describe().endswith("mtk_attn_fwd_d64_f16_causal")
+    # D = 64 exactly: the ping-pong kernel for non-causal grids that fill the device, as at D = 128
+    p64 = mtk.AttentionPlan(None, 2, 32, 4096, 4096, 64)
+    assert p64.describe().endswith("kernels: mtk_attn_fwd_pp_d64_f16") and "rows/wg=256 grid=1024" in p64.describe()
+    assert mtk.AttentionPlan(None, 2, 32, 4096, 4096, 64, q_rows=128).describe().endswith("kernels: mtk_attn_fwd_d64_f16")
+    assert mtk.AttentionPlan(None, 1, 2, 300, 300, 64, causal=True, q_rows=256, dtype="bf16").describe().endswith(
+        "kernels: mtk_attn_fwd_pp_d64_bf16_causal")
     for D, q_rows, status in ((257, 0, mtk.MTK_ERR_UNSUPPORTED), (0, 0, mtk.MTK_ERR_UNSUPPORTED),
-                              (64, 256, mtk.MTK_ERR_UNSUPPORTED)):
+                              (56, 256, mtk.MTK_ERR_UNSUPPORTED), (96, 256, mtk.MTK_ERR_UNSUPPORTED)):
         with pytest.raises(mtk.MtkError) as e:
             mtk.AttentionPlan(None, 1, 1, 16, 16, D, q_rows=q_rows)
         assert e.value.status == status

@@ -62,6 +62,27 @@ def test_head_dim_grouped_kv(dev, D, causal):
     assert np.array_equal(got.view(np.uint16), full.view(np.uint16))
 
 
+@pytest.mark.parametrize("S,Skv", [(1, 1), (255, 256), (300, 270), (513, 700), (1000, 1000)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_d64_ping_pong(dev, S, Skv, causal, dtype):
+    # the 256-query ping-pong kernel at D = 64 (the plan's choice for non-causal grids that fill the
+    # device): against the oracle, and bit for bit against the 128-query kernel, whose arithmetic
+    # it shares
+    Q, K, V = qkv_d(500 + S, 2, S, 3, 64, Skv=Skv, dtype=dtype)
+    got, _ = check(dev, Q, K, V, causal, dtype=dtype, label=f"D64 q_rows=256 {S}x{Skv}", q_rows=256)
+    ref = mtk.attention(dev, Q, K, V, causal=causal, dtype=dtype, q_rows=128)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_d64_ping_pong_grouped_kv(dev, causal):
+    Q, K, V = qkv_d(71, 2, 400, 8, 64, Skv=330, Hkv=2)
+    got, _ = check(dev, Q, K, V, causal, label="D64 q_rows=256 H8/Hkv2", q_rows=256)
+    full = mtk.attention(dev, Q, np.repeat(K, 4, 2), np.repeat(V, 4, 2), causal=causal, q_rows=128)
+    assert np.array_equal(got.view(np.uint16), full.view(np.uint16))
+
+
 @pytest.mark.parametrize("D", [64, 96, 256, 37, 512])
 def test_head_dim_closed_forms(dev, D):
     B, S, H = 1, 200, 2
@@ -112,8 +133,8 @@ def test_head_dim_limits(dev):
         with pytest.raises(mtk.MtkError) as e:
             mtk.AttentionPlan(dev, 1, 1, 16, 16, D)
         assert e.value.status == mtk.MTK_ERR_UNSUPPORTED
-    with pytest.raises(mtk.MtkError):  # the ping-pong kernel is for D = 128 only
-        mtk.AttentionPlan(dev, 1, 1, 16, 16, 64, q_rows=256)
+    with pytest.raises(mtk.MtkError):  # the ping-pong kernel is for D = 128 and 64 only
+        mtk.AttentionPlan(dev, 1, 1, 16, 16, 96, q_rows=256)
     with pytest.raises(mtk.MtkError):  # D above 256: 64 query rows per workgroup, chosen by the plan
         mtk.AttentionPlan(dev, 1, 1, 16, 16, 264, q_rows=128)
     assert "rows/wg=64 " in mtk.AttentionPlan(dev, 1, 2, 100, 100, 512).describe()
