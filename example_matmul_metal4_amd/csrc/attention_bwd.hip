@@ -1,6 +1,7 @@
 // Flash-attention backward for gfx950 (head dimensions that are multiples of 8 up to 128: the
-// kernels are laid out for 128, chunks of 8 elements past D are loaded as zeros, contribute exact
-// zeros to every product, and are not stored), fp16/bf16 in and out, fp32 accumulate.
+// kernels are templated on a padded head dimension DP of 64 or 128, chunks of 8 elements past D are
+// loaded as zeros, contribute exact zeros to every product, and are not stored), fp16/bf16 in and
+// out, fp32 accumulate.
 //
 // The reference has no GPU backward; its CPU restatement of the gradients of the loss
 // Phi = sum dO * O is Sources/attention/Network.swift:205-281 (dP row, D-term, dS row) and
@@ -22,19 +23,20 @@
 //                  accumulators as the B operands of dV^T += dO^T.P and dK^T += Q^T.dS, whose
 //                  A operands are transposed LDS reads (ds_read_b64_tr_b16) of the dO / Q tiles.
 //                  Software-pipelined: the S / dP MFMAs of tile i + 1 run interleaved with the
-//                  softmax work of tile i (one element per MFMA), then the dV / dK MFMAs of tile i.
+//                  softmax work of tile i (one or two elements per MFMA), then the dV / dK MFMAs
+//                  of tile i.
 //   attn_bwd_dq    one workgroup per 256 queries, 8 wavefronts x 32 queries (the forward's shape):
 //                  S^T = K.Q^T and dP^T = V.dO^T with the query as the accumulator column, then
 //                  dQ^T += K^T.dS^T with K^T read transposed from LDS.
-// Each LDS operand tile is 64 rows of 256 bytes; tiles read as rows use the chunk swizzle
-// chunk ^ (row & 15), tiles read transposed chunk ^ 4 * (row & 3) (both conflict-free, as in the
-// forward); an operand read both ways is staged twice.
-#include "device.hpp"
+// Each LDS operand tile is 64 rows of 2 DP bytes with the forward's swizzles for that width
+// (AttnLayout): at DP = 128 tiles read as rows use the chunk swizzle chunk ^ (row & 15), tiles read
+// transposed chunk ^ 4 * (row & 3); at DP = 64 (two rows per 256-byte bank line) chunk ^ ((row >> 1)
+// & 7) and chunk ^ 4 * ((row >> 1) & 1) (all conflict-free); an operand read both ways is staged
+// twice.
+#include "attention.hpp"  // AttnLayout: the LDS row layouts and swizzles shared with the forward
 
 namespace mtk {
 
-constexpr int kBD = 128;                 // padded head dimension
-constexpr int kRowTile = 64 * kBD * 2;   // one 64-row operand tile in LDS: 16 KB
 constexpr int kBwdKeys = 128;            // keys per dK/dV workgroup
 constexpr int kBwdQTile = 64;            // queries per LDS tile of the dK/dV kernel
 constexpr int kBwdQRows = 256;           // queries per dQ workgroup
@@ -42,27 +44,33 @@ constexpr int kBwdKTile = 64;            // keys per LDS tile of the dQ kernel
 
 __device__ __forceinline__ int bwd_swap_bits_2_3(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
-// Row-read tile: byte offset of 16-byte chunk `chunk` of row `row`.
+// Row-read tile (rows of DP elements): byte offset of 16-byte chunk `chunk` of row `row`.
+template <int DP>
 __device__ __forceinline__ uint32_t row_off(int row, int chunk) {
-  return (uint32_t)(row * 256 + ((chunk ^ (row & 15)) << 4));
+  using L = AttnLayout<DP>;
+  return (uint32_t)(row * L::kRowB + ((chunk ^ L::kswz(row)) << 4));
 }
 
 // Transposed-read fragment base for d block db: lane (h = lane / 16, s = lane % 16) reads rows
 // 8 (h / 2) + s / 4 (+ 4 e, + 16 js) at d = 32 db + 16 (h & 1) + 4 (s & 3); the result is the A
 // operand [32 d][16 rows] of a 32x32x16 MFMA: lane gets d = 32 db + lane % 32 at rows
 // 16 js + 8 (lane / 32) + 0..7.
+// (The swizzle of the base row holds for the rows 4 and 16 js further on.)
+template <int DP>
 __device__ __forceinline__ uint32_t tr_base(const char *tile, int db, int lane) {
+  using L = AttnLayout<DP>;
   const int s = lane & 15, h = lane >> 4;
   const int d = 32 * db + 16 * (h & 1) + 4 * (s & 3);
   const int row = 8 * (h >> 1) + (s >> 2);
-  return lds_addr(tile) + (uint32_t)(row * 256 + 16 * ((d >> 3) ^ (4 * (row & 3))) + 2 * (d & 7));
+  return lds_addr(tile) + (uint32_t)(row * L::kRowB + 16 * ((d >> 3) ^ L::vswz(row)) + 2 * (d & 7));
 }
 
 // Transposed fragment for row step js (16 rows) from a base made by tr_base (+ a tile offset).
-template <int JS>
+template <int DP, int JS>
 __device__ __forceinline__ u32x4 tr_frag(uint32_t base) {
-  const u32x2 w0 = ds_read_tr16_at<4096 * JS>(base);
-  const u32x2 w1 = ds_read_tr16_at<4096 * JS + 1024>(base);
+  constexpr int R = AttnLayout<DP>::kRowB;
+  const u32x2 w0 = ds_read_tr16_at<16 * R * JS>(base);
+  const u32x2 w1 = ds_read_tr16_at<16 * R * JS + 4 * R>(base);
   return u32x4{w0.x, w0.y, w1.x, w1.y};
 }
 
@@ -82,19 +90,21 @@ __device__ __forceinline__ void lgkm_wait_n(u32x4 &f) {
   asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(f) : "n"(N));
 }
 
-// Stage rows [row0, row0 + 4 * n) of a 64-row operand tile: instruction i fills 4 rows (1 KB),
-// lane l writes row row0 + 4 i + l / 16, LDS chunk l % 16, which holds global chunk
-// (l % 16) ^ swizzle(row). Rows at or past `rows_valid` and chunks at or past `nchunk` (head
-// dimensions below 128: 8 elements per chunk) read zero.
-template <int N, bool TR>
+// Stage rows [row0, row0 + R n) of a 64-row operand tile (R = 1024 / row bytes: 4 rows of 256
+// bytes, or 8 of 128): instruction i fills R rows (1 KB), lane l writes row row0 + R i + l / C,
+// LDS chunk l % C (C chunks per row), which holds global chunk (l % C) ^ swizzle(row). Rows at or
+// past `rows_valid` and chunks at or past `nchunk` (head dimensions below DP: 8 elements per
+// chunk) read zero.
+template <int DP, int N, bool TR>
 __device__ __forceinline__ void stage_rows(rsrc_t r, char *tile, int row0, uint32_t base, uint32_t rs, int rows_valid,
                                            int nchunk, int lane) {
+  using L = AttnLayout<DP>;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    const int row = row0 + 4 * i + (lane >> 4);
-    const int pc = lane & 15;
-    const int gc = TR ? (pc ^ (4 * (row & 3))) : (pc ^ (row & 15));
-    lds_direct16(r, tile + (row0 + 4 * i) * 256,
+    const int row = row0 + L::kRpi * i + (int)((unsigned)lane / L::kCpr);
+    const int pc = (int)((unsigned)lane % L::kCpr);
+    const int gc = TR ? (pc ^ L::vswz(row)) : (pc ^ L::kswz(row));
+    lds_direct16(r, tile + (row0 + L::kRpi * i) * L::kRowB,
                  row < rows_valid && gc < nchunk ? base + (uint32_t)row * rs + 16u * gc : kOOB);
   }
 }
@@ -137,8 +147,10 @@ __device__ __forceinline__ void attn_bwd_pre(const mtk_attn_bwd_kargs &a) {
 
 // ------------------------------------------------------------------------------------- dK, dV
 
-template <int DT, bool CAUSAL>
+template <int DT, bool CAUSAL, int DP>
 __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
+  using L = AttnLayout<DP>;
+  constexpr int kRowTile = L::kTile, kRowB = L::kRowB, kKs = L::kKs, kDb = L::kDb;
   // LDS: two slots of (Q rows, dO rows) read by S = Q.K^T and dP = dO.V^T, two slots of (Q, dO
   // transposed-read copies) read by dV and dK, two slots of a tile's 64 lse and 64 D values. Step
   // i's row tiles are read one step before its transposed tiles: the S / dP MFMAs of step i + 1 run
@@ -158,7 +170,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   const int b = bh / a.H_kv, hk = bh - b * a.H_kv;
   const int group = a.H / a.H_kv;  // query heads hk * group .. hk * group + group - 1
   const int k0 = kb * kBwdKeys;
-  // rows of D elements (a multiple of 8, at most 128): chunks at or past nchunk are zeros
+  // rows of D elements (a multiple of 8, at most DP): chunks at or past nchunk are zeros
   const int nchunk = a.D >> 3;
   const uint32_t rs = (uint32_t)a.H * a.D * 2, rkv = (uint32_t)a.H_kv * a.D * 2;
   const uint32_t kvbase = (uint32_t)(((size_t)b * a.S_kv * a.H_kv + hk) * a.D * 2);
@@ -172,12 +184,12 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   const int diag = a.S_kv - a.S_q;  // key j is visible to query i iff j <= i + diag (causal)
   const float c = a.scale_log2;
 
-  // this lane's key (accumulator column) and its K / V rows as B operands (8 steps of 16 dims)
+  // this lane's key (accumulator column) and its K / V rows as B operands (steps of 16 dims)
   const int key = k0 + wave * 32 + col;
   const bool key_ok = key < a.S_kv;
-  u32x4 kf[8], vf[8];
+  u32x4 kf[kKs], vf[kKs];
 #pragma unroll
-  for (int ds = 0; ds < 8; ++ds) {
+  for (int ds = 0; ds < kKs; ++ds) {
     const uint32_t off = key_ok && 2 * ds + g < nchunk ? kvbase + (uint32_t)key * rkv + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB;
     kf[ds] = buf_load16(rk, off);
     vf[ds] = buf_load16(rv, off);
@@ -207,16 +219,16 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     int valid, t;
     uint32_t tb, row_base;
     tile_of(i, valid, tb, row_base, t);
-    stage_rows<4, false>(rq, st, 16 * wave, tb, rs, valid, nchunk, lane);
-    stage_rows<4, false>(rg, st + kRowTile, 16 * wave, tb, rs, valid, nchunk, lane);
+    stage_rows<DP, 16 / L::kRpi, false>(rq, st, 16 * wave, tb, rs, valid, nchunk, lane);
+    stage_rows<DP, 16 / L::kRpi, false>(rg, st + kRowTile, 16 * wave, tb, rs, valid, nchunk, lane);
   };
   auto stage_tr_to = [&](int slot, int i) {
     char *st = smem + kTrOff + slot * kPair;
     int valid, t;
     uint32_t tb, row_base;
     tile_of(i, valid, tb, row_base, t);
-    stage_rows<4, true>(rq, st, 16 * wave, tb, rs, valid, nchunk, lane);
-    stage_rows<4, true>(rg, st + kRowTile, 16 * wave, tb, rs, valid, nchunk, lane);
+    stage_rows<DP, 16 / L::kRpi, true>(rq, st, 16 * wave, tb, rs, valid, nchunk, lane);
+    stage_rows<DP, 16 / L::kRpi, true>(rg, st + kRowTile, 16 * wave, tb, rs, valid, nchunk, lane);
     // lse (wave 0) and D (wave 1) of the tile's queries: lanes 0-15 load 4 values each (entries past
     // S_q are never used unmasked); lanes 16-63 write zeros
     if (wave < 2) {
@@ -227,18 +239,20 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
 
   // A-operand rows of S = Q.K^T / dP = dO.V^T: MFMA row m reads query swap_bits_2_3(m) of the block
   const int arow = bwd_swap_bits_2_3(col);
-  f32x16 dk[4], dv[4];
+  f32x16 dk[kDb], dv[kDb];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kDb; ++i) {
     dk[i] = f32x16{};
     dv[i] = f32x16{};
   }
 
   // S and dP of the step whose rows are in rows slot `slot`, for the two 32-query blocks of the
-  // tile: 32 MFMAs in four interleaved accumulation chains (step k: d step k / 4; S of block 0, dP
-  // of block 0, S of block 1, dP of block 1), each operand fragment read kBwdSdpAhead steps
-  // ahead of its MFMA; after MFMA k, vstep(k) runs one element of the previous step's softmax.
-  // The fence per step keeps that order; every chain still accumulates its d steps in order.
+  // tile: 4 kKs MFMAs in four interleaved accumulation chains (step k: d step k / 4; S of block 0,
+  // dP of block 0, S of block 1, dP of block 1), each operand fragment read kBwdSdpAhead steps
+  // ahead of its MFMA; after MFMA k, vstep runs 32 / (4 kKs) of the 32 elements of the previous
+  // step's softmax. The fence per step keeps that order; every chain still accumulates its d steps
+  // in order.
+  constexpr int kSdpSteps = 4 * kKs, kElPerStep = 32 / kSdpSteps;
   auto sdp = [&](int slot, f32x16 (&s_)[2], f32x16 (&p_)[2], auto &&vstep) {
     const char *qrow = smem + kRowsOff + slot * kPair, *grow = qrow + kRowTile;
 #pragma unroll
@@ -249,12 +263,12 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     constexpr int D = kBwdSdpAhead;
     auto rdf = [&](int k) {
       const int ds = k >> 2, qb = (k >> 1) & 1;
-      return *(const u32x4 *)(((k & 1) ? grow : qrow) + row_off(32 * qb + arow, 2 * ds + g));
+      return *(const u32x4 *)(((k & 1) ? grow : qrow) + row_off<DP>(32 * qb + arow, 2 * ds + g));
     };
     u32x4 fr[D];
 #pragma unroll
     for (int k = 0; k < D; ++k) fr[k] = rdf(k);
-    static_for<0, 32>([&](auto kc) {
+    static_for<0, kSdpSteps>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
       __builtin_amdgcn_sched_barrier(0);
       constexpr int ds = k >> 2, qb = (k >> 1) & 1;
@@ -262,8 +276,8 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
         p_[qb] = mfma32x32x16<DT>(fr[k % D], vf[ds], p_[qb]);
       else
         s_[qb] = mfma32x32x16<DT>(fr[k % D], kf[ds], s_[qb]);
-      vstep(kc);
-      if constexpr (k + D < 32) fr[k % D] = rdf(k + D);
+      static_for<0, kElPerStep>([&](auto ec) { vstep(std::integral_constant<int, k * kElPerStep + decltype(ec)::value>{}); });
+      if constexpr (k + D < kSdpSteps) fr[k % D] = rdf(k + D);
     });
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -341,35 +355,35 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
     else
       sdp(nslot, s2, p2, soft(std::false_type{}));
 
-    // dV^T += dO^T . P and dK^T += Q^T . dS: 32 MFMAs in eight interleaved accumulation chains
-    // (step k: 16-query step js = k / 8, d block (k / 2) % 4, dV for even k, dK for odd k), each
-    // transposed operand fragment read kBwdTrAhead steps ahead; every dV[db] / dK[db] still
-    // accumulates js = 0..3 in order.
+    // dV^T += dO^T . P and dK^T += Q^T . dS: 8 kDb MFMAs in 2 kDb interleaved accumulation
+    // chains (step k: 16-query step js = k / (2 kDb), d block (k / 2) % kDb, dV for even k, dK for
+    // odd k), each transposed operand fragment read kBwdTrAhead steps ahead; every dV[db] / dK[db]
+    // still accumulates js = 0..3 in order.
     {
-      constexpr int D = kBwdTrAhead;
-      uint32_t tb[8];
+      constexpr int D = kBwdTrAhead, kTrSteps = 8 * kDb;
+      uint32_t tb[2 * kDb];
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        tb[2 * db] = tr_base(gtr, db, lane);
-        tb[2 * db + 1] = tr_base(qtr, db, lane);
+      for (int db = 0; db < kDb; ++db) {
+        tb[2 * db] = tr_base<DP>(gtr, db, lane);
+        tb[2 * db + 1] = tr_base<DP>(qtr, db, lane);
       }
       u32x4 tf[D];
       auto rdt = [&](auto kc) {
         constexpr int K = decltype(kc)::value;
-        tf[K % D] = tr_frag<K / 8>(tb[K & 7]);
+        tf[K % D] = tr_frag<DP, K / (2 * kDb)>(tb[K % (2 * kDb)]);
       };
       static_for<0, D>([&](auto kc) { rdt(kc); });
-      static_for<0, 32>([&](auto kc) {
+      static_for<0, kTrSteps>([&](auto kc) {
         constexpr int K = decltype(kc)::value;
-        constexpr int kAfter = (31 - K) < (D - 1) ? (31 - K) : (D - 1);  // fragments read after K
+        constexpr int kAfter = (kTrSteps - 1 - K) < (D - 1) ? (kTrSteps - 1 - K) : (D - 1);  // fragments read after K
         __builtin_amdgcn_sched_barrier(0);
         lgkm_wait_n<2 * kAfter>(tf[K % D]);
-        constexpr int js = K / 8, db = (K >> 1) & 3;
+        constexpr int js = K / (2 * kDb), db = (K >> 1) % kDb;
         if constexpr (K & 1)
           dk[db] = mfma32x32x16<DT>(tf[K % D], sb[js], dk[db]);
         else
           dv[db] = mfma32x32x16<DT>(tf[K % D], pb[js], dv[db]);
-        if constexpr (K + D < 32) rdt(std::integral_constant<int, K + D>{});
+        if constexpr (K + D < kTrSteps) rdt(std::integral_constant<int, K + D>{});
       });
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -381,19 +395,19 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   }
 
   // dK[key][d], dV[key][d]: lane = key, register 4 rq + e of block db = d 32 db + 8 rq + 4 g + e.
-  // The tiles go through LDS (free after the loop): each wave parks its 32 keys as 256-byte rows
-  // (16-byte chunk c of row r at chunk c ^ (r & 15)), then stores whole rows, 16 bytes per lane, so
-  // every store instruction writes four complete rows instead of 8-byte pieces of 32 rows.
+  // The tiles go through LDS (free after the loop): each wave parks its 32 keys as rows of DP
+  // elements (16-byte chunk c of row r at chunk c ^ kswz(r)), then stores whole rows, 16 bytes per
+  // lane, so every store instruction writes complete rows instead of 8-byte pieces of 32 rows.
   // The last iterations issue clamped loads past the end into the stages; they must have landed
   // before the stages are reused for the output tiles (explicit, not left to the fence's own wait).
   wait_vmem();
   __syncthreads();  // every wave is done reading the last stage
-  char *pk = smem + wave * (2 * 32 * 256), *pv = pk + 32 * 256;
+  char *pk = smem + wave * (2 * 32 * kRowB), *pv = pk + 32 * kRowB;
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < kDb; ++db)
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
-      const uint32_t o = (uint32_t)(col * 256 + (((4 * db + rq) ^ (col & 15)) << 4) + 8 * g);
+      const uint32_t o = (uint32_t)(col * kRowB + (((4 * db + rq) ^ L::kswz(col)) << 4) + 8 * g);
       *(u32x2 *)(pk + o) = u32x2{pack2<DT>(dk[db][4 * rq], dk[db][4 * rq + 1]),
                                  pack2<DT>(dk[db][4 * rq + 2], dk[db][4 * rq + 3])};
       *(u32x2 *)(pv + o) = u32x2{pack2<DT>(dv[db][4 * rq], dv[db][4 * rq + 1]),
@@ -404,10 +418,10 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
   uint16_t *dV = (uint16_t *)a.dV;
   const size_t base0 = ((size_t)b * a.S_kv * a.H_kv + hk) * a.D;
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int r = 4 * it + (lane >> 4), pc = lane & 15;
+  for (int it = 0; it < 32 / L::kRpi; ++it) {
+    const int r = L::kRpi * it + (int)((unsigned)lane / L::kCpr), pc = (int)((unsigned)lane % L::kCpr);
     const int kr = k0 + wave * 32 + r;
-    const uint32_t o = (uint32_t)(r * 256 + ((pc ^ (r & 15)) << 4));
+    const uint32_t o = (uint32_t)(r * kRowB + ((pc ^ L::kswz(r)) << 4));
     const u32x4 vk = *(const u32x4 *)(pk + o), vv = *(const u32x4 *)(pv + o);
     if (kr < a.S_kv && pc < nchunk) {
       const size_t e = base0 + (size_t)kr * a.H_kv * a.D + 8 * pc;
@@ -419,8 +433,10 @@ __device__ __forceinline__ void attn_bwd_dkdv(const mtk_attn_bwd_kargs &a) {
 
 // ------------------------------------------------------------------------------------- dQ
 
-template <int DT, bool CAUSAL>
+template <int DT, bool CAUSAL, int DP>
 __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
+  using L = AttnLayout<DP>;
+  constexpr int kRowTile = L::kTile, kRowB = L::kRowB, kKs = L::kKs, kDb = L::kDb;
   // per stage: K rows, K transposed-read copy, V rows
   __shared__ __attribute__((aligned(1024))) char smem[2 * 3 * kRowTile];
 
@@ -452,9 +468,9 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
   // this lane's query (accumulator column): Q and dO rows as B operands, its lse and D
   const int qi = q0 + wave * 32 + col;
   const bool q_ok = qi < a.S_q;
-  u32x4 qf[8], gf[8];
+  u32x4 qf[kKs], gf[kKs];
 #pragma unroll
-  for (int ds = 0; ds < 8; ++ds) {
+  for (int ds = 0; ds < kKs; ++ds) {
     const uint32_t off = q_ok && 2 * ds + g < nchunk ? qbase + (uint32_t)qi * rs + (uint32_t)(16 * ds + 8 * g) * 2u : kOOB;
     qf[ds] = buf_load16(rq, off);
     gf[ds] = buf_load16(rg, off);
@@ -471,15 +487,15 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
     char *st = smem + slot * 3 * kRowTile;
     const int valid = a.S_kv - t * kBwdKTile;
     const uint32_t tb = kvbase + (uint32_t)(t * kBwdKTile) * rkv;
-    stage_rows<2, false>(rk, st, 8 * wave, tb, rkv, valid, nchunk, lane);
-    stage_rows<2, true>(rk, st + kRowTile, 8 * wave, tb, rkv, valid, nchunk, lane);
-    stage_rows<2, false>(rv, st + 2 * kRowTile, 8 * wave, tb, rkv, valid, nchunk, lane);
+    stage_rows<DP, 8 / L::kRpi, false>(rk, st, 8 * wave, tb, rkv, valid, nchunk, lane);
+    stage_rows<DP, 8 / L::kRpi, true>(rk, st + kRowTile, 8 * wave, tb, rkv, valid, nchunk, lane);
+    stage_rows<DP, 8 / L::kRpi, false>(rv, st + 2 * kRowTile, 8 * wave, tb, rkv, valid, nchunk, lane);
   };
 
   const int arow = bwd_swap_bits_2_3(col);  // MFMA row m reads key swap_bits_2_3(m) of the block
-  f32x16 dq[4];
+  f32x16 dq[kDb];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) dq[i] = f32x16{};
+  for (int i = 0; i < kDb; ++i) dq[i] = f32x16{};
 
   if (n_tiles > 0) stage(0, 0);
   for (int t = 0; t < n_tiles; ++t) {
@@ -498,26 +514,26 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
     const bool need_mask = wave_q0 + 31 >= a.S_q || j0 + kBwdKTile > a.S_kv || (CAUSAL && j0 + kBwdKTile - 1 > wave_q0 + diag);
     static_for<0, 2>([&](auto kc) {
       constexpr int kb = decltype(kc)::value;
-      // S^T and dP^T: 16 MFMAs in two chains (step k: d step k / 2, S for even k, dP for odd k),
-      // each fragment read kDqSdpAhead steps ahead; the fence per step keeps that order
+      // S^T and dP^T: 2 kKs MFMAs in two chains (step k: d step k / 2, S for even k, dP for odd
+      // k), each fragment read kDqSdpAhead steps ahead; the fence per step keeps that order
       f32x16 s = f32x16{}, p = f32x16{};
       {
         constexpr int D = kDqSdpAhead;
         auto rdf = [&](int k) {
-          return *(const u32x4 *)(((k & 1) ? vrow : krow) + row_off(32 * kb + arow, 2 * (k >> 1) + g));
+          return *(const u32x4 *)(((k & 1) ? vrow : krow) + row_off<DP>(32 * kb + arow, 2 * (k >> 1) + g));
         };
         u32x4 fr[D];
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int k = 0; k < D; ++k) fr[k] = rdf(k);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
+        for (int k = 0; k < 2 * kKs; ++k) {
           __builtin_amdgcn_sched_barrier(0);
           if (k & 1)
             p = mfma32x32x16<DT>(fr[k % D], gf[k >> 1], p);
           else
             s = mfma32x32x16<DT>(fr[k % D], qf[k >> 1], s);
-          if (k + D < 16) fr[k % D] = rdf(k + D);
+          if (k + D < 2 * kKs) fr[k % D] = rdf(k + D);
         }
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
@@ -548,27 +564,27 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
       else
         softmax_half(std::false_type{});
 
-      // dQ^T += K^T . dS^T for key steps 2 kb, 2 kb + 1: 8 MFMAs (step K: d block K / 2, key step
-      // 2 kb + K % 2), each transposed fragment read kDqTrAhead steps ahead
+      // dQ^T += K^T . dS^T for key steps 2 kb, 2 kb + 1: 2 kDb MFMAs (step K: d block K / 2, key
+      // step 2 kb + K % 2), each transposed fragment read kDqTrAhead steps ahead
       {
-        constexpr int D = kDqTrAhead;
-        uint32_t tb[4];
+        constexpr int D = kDqTrAhead < 2 * kDb ? kDqTrAhead : 2 * kDb, kQSteps = 2 * kDb;
+        uint32_t tb[kDb];
 #pragma unroll
-        for (int db = 0; db < 4; ++db) tb[db] = tr_base(ktr, db, lane);
+        for (int db = 0; db < kDb; ++db) tb[db] = tr_base<DP>(ktr, db, lane);
         u32x4 tf[D];
         auto rdt = [&](auto kc2) {
           constexpr int K = decltype(kc2)::value;
-          tf[K % D] = tr_frag<2 * kb + (K & 1)>(tb[K >> 1]);
+          tf[K % D] = tr_frag<DP, 2 * kb + (K & 1)>(tb[K >> 1]);
         };
         static_for<0, D>([&](auto kc2) { rdt(kc2); });
         __builtin_amdgcn_s_setprio(1);
-        static_for<0, 8>([&](auto kc2) {
+        static_for<0, kQSteps>([&](auto kc2) {
           constexpr int K = decltype(kc2)::value;
-          constexpr int kAfter = (7 - K) < (D - 1) ? (7 - K) : (D - 1);  // fragments read after K
+          constexpr int kAfter = (kQSteps - 1 - K) < (D - 1) ? (kQSteps - 1 - K) : (D - 1);  // fragments read after K
           __builtin_amdgcn_sched_barrier(0);
           lgkm_wait_n<2 * kAfter>(tf[K % D]);
           dq[K >> 1] = mfma32x32x16<DT>(tf[K % D], sb[K & 1], dq[K >> 1]);
-          if constexpr (K + D < 8) rdt(std::integral_constant<int, K + D>{});
+          if constexpr (K + D < kQSteps) rdt(std::integral_constant<int, K + D>{});
         });
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(0);
@@ -577,23 +593,23 @@ __device__ __forceinline__ void attn_bwd_dq(const mtk_attn_bwd_kargs &a) {
   }
 
   // dQ[qi][d]: lane = query, register 4 rq + e of block db = d 32 db + 8 rq + 4 g + e; parked in
-  // LDS as 256-byte rows and stored as whole rows, as in the dK/dV kernel (no loads are in flight
+  // LDS as rows of DP elements and stored as whole rows, as in the dK/dV kernel (no loads are in flight
   // here: the loop stages no tile past the last and waits for each tile it staged)
   __syncthreads();  // every wave is done reading the last stage
-  char *pq = smem + wave * (32 * 256);
+  char *pq = smem + wave * (32 * kRowB);
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+  for (int db = 0; db < kDb; ++db)
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq)
-      *(u32x2 *)(pq + col * 256 + (((4 * db + rq) ^ (col & 15)) << 4) + 8 * g) =
+      *(u32x2 *)(pq + col * kRowB + (((4 * db + rq) ^ L::kswz(col)) << 4) + 8 * g) =
           u32x2{pack2<DT>(dq[db][4 * rq], dq[db][4 * rq + 1]), pack2<DT>(dq[db][4 * rq + 2], dq[db][4 * rq + 3])};
   __syncthreads();
   uint16_t *dQ = (uint16_t *)a.dQ;
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int r = 4 * it + (lane >> 4), pc = lane & 15;
+  for (int it = 0; it < 32 / L::kRpi; ++it) {
+    const int r = L::kRpi * it + (int)((unsigned)lane / L::kCpr), pc = (int)((unsigned)lane % L::kCpr);
     const int qr = q0 + wave * 32 + r;
-    const u32x4 v = *(const u32x4 *)(pq + r * 256 + ((pc ^ (r & 15)) << 4));
+    const u32x4 v = *(const u32x4 *)(pq + r * kRowB + ((pc ^ L::kswz(r)) << 4));
     if (qr < a.S_q && pc < nchunk) *(u32x4 *)(dQ + (((size_t)b * a.S_q + qr) * a.H + h) * a.D + 8 * pc) = v;
   }
 }
@@ -604,22 +620,31 @@ using namespace mtk;
 
 #define BWD_PRE(NAME, DT) \
   extern "C" __global__ void __launch_bounds__(256) NAME(const mtk_attn_bwd_kargs a) { attn_bwd_pre<DT>(a); }
-#define BWD_DKDV(NAME, DT, CAUSAL)                                                   \
+#define BWD_DKDV(NAME, DT, CAUSAL, DP)                                               \
   extern "C" __global__ void __launch_bounds__(256) NAME(const mtk_attn_bwd_kargs a) { \
-    attn_bwd_dkdv<DT, CAUSAL>(a);                                                    \
+    attn_bwd_dkdv<DT, CAUSAL, DP>(a);                                                \
   }
-#define BWD_DQ(NAME, DT, CAUSAL)                                                     \
+#define BWD_DQ(NAME, DT, CAUSAL, DP)                                                 \
   extern "C" __global__ void __launch_bounds__(512) NAME(const mtk_attn_bwd_kargs a) { \
-    attn_bwd_dq<DT, CAUSAL>(a);                                                      \
+    attn_bwd_dq<DT, CAUSAL, DP>(a);                                                  \
   }
 
 BWD_PRE(mtk_attn_bwd_pre_f16, DT_F16)
 BWD_PRE(mtk_attn_bwd_pre_bf16, DT_BF16)
-BWD_DKDV(mtk_attn_bwd_dkdv_f16, DT_F16, false)
-BWD_DKDV(mtk_attn_bwd_dkdv_bf16, DT_BF16, false)
-BWD_DKDV(mtk_attn_bwd_dkdv_f16_causal, DT_F16, true)
-BWD_DKDV(mtk_attn_bwd_dkdv_bf16_causal, DT_BF16, true)
-BWD_DQ(mtk_attn_bwd_dq_f16, DT_F16, false)
-BWD_DQ(mtk_attn_bwd_dq_bf16, DT_BF16, false)
-BWD_DQ(mtk_attn_bwd_dq_f16_causal, DT_F16, true)
-BWD_DQ(mtk_attn_bwd_dq_bf16_causal, DT_BF16, true)
+BWD_DKDV(mtk_attn_bwd_dkdv_f16, DT_F16, false, 128)
+BWD_DKDV(mtk_attn_bwd_dkdv_bf16, DT_BF16, false, 128)
+BWD_DKDV(mtk_attn_bwd_dkdv_f16_causal, DT_F16, true, 128)
+BWD_DKDV(mtk_attn_bwd_dkdv_bf16_causal, DT_BF16, true, 128)
+BWD_DQ(mtk_attn_bwd_dq_f16, DT_F16, false, 128)
+BWD_DQ(mtk_attn_bwd_dq_bf16, DT_BF16, false, 128)
+BWD_DQ(mtk_attn_bwd_dq_f16_causal, DT_F16, true, 128)
+BWD_DQ(mtk_attn_bwd_dq_bf16_causal, DT_BF16, true, 128)
+// head dimensions up to 64: the same kernels laid out for 64 (rows of 128 bytes)
+BWD_DKDV(mtk_attn_bwd_dkdv_d64_f16, DT_F16, false, 64)
+BWD_DKDV(mtk_attn_bwd_dkdv_d64_bf16, DT_BF16, false, 64)
+BWD_DKDV(mtk_attn_bwd_dkdv_d64_f16_causal, DT_F16, true, 64)
+BWD_DKDV(mtk_attn_bwd_dkdv_d64_bf16_causal, DT_BF16, true, 64)
+BWD_DQ(mtk_attn_bwd_dq_d64_f16, DT_F16, false, 64)
+BWD_DQ(mtk_attn_bwd_dq_d64_bf16, DT_BF16, false, 64)
+BWD_DQ(mtk_attn_bwd_dq_d64_f16_causal, DT_F16, true, 64)
+BWD_DQ(mtk_attn_bwd_dq_d64_bf16_causal, DT_BF16, true, 64)

@@ -453,9 +453,10 @@ int plan_attn_bwd(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
     return fail(MTK_ERR_INVALID, "H_kv must divide H (got H=%d, H_kv=%d)", d.H, d.H_kv);
   if (d.D <= 0 || d.D > 256 || d.D % 8 != 0)
     return fail(MTK_ERR_UNSUPPORTED, "backward head dimension must be a multiple of 8 up to 256 (got %d)", d.D);
-  // D <= 128: the 32-key / 32-query wavefront kernels laid out for 128 (chunks past D are zeros);
-  // 128 < D <= 256: the 16-key / 16-query wavefront kernels laid out for 256
+  // D <= 128: the 32-key / 32-query wavefront kernels, laid out for 64 (D <= 64) or 128 (chunks
+  // past D are zeros); 128 < D <= 256: the 16-key / 16-query wavefront kernels laid out for 256
   const bool wide = d.D > 128;
+  const char *lay = d.D <= 64 ? "d64_" : "";
   if (d.dtype != MTK_F16 && d.dtype != MTK_BF16) return fail(MTK_ERR_INVALID, "attention dtype must be MTK_F16 or MTK_BF16");
   if (d.q_rows != 0) return fail(MTK_ERR_INVALID, "the backward plan chooses its own blocking (q_rows must be 0)");
   const uint64_t q_bytes = (uint64_t)d.B * d.S_q * d.H * d.D * 2;
@@ -486,9 +487,9 @@ int plan_attn_bwd(mtk_ctx *ctx, const mtk_attn_desc *d_in, mtk_plan **out) {
   Launch pre, kv, q;
   pre.name = std::string("mtk_attn_bwd_pre_") + dt;
   pre.grid = (unsigned)(((long long)d.B * d.S_q * d.H + 15) / 16);
-  kv.name = std::string(wide ? "mtk_attn_bwd256_dkdv_" : "mtk_attn_bwd_dkdv_") + dt + cz;
+  kv.name = std::string(wide ? "mtk_attn_bwd256_dkdv_" : "mtk_attn_bwd_dkdv_") + (wide ? "" : lay) + dt + cz;
   kv.grid = (unsigned)((long long)a.k_blocks * d.B * d.H_kv);  // per K/V head: sums over its query heads
-  q.name = std::string(wide ? "mtk_attn_bwd256_dq_" : "mtk_attn_bwd_dq_") + dt + cz;
+  q.name = std::string(wide ? "mtk_attn_bwd256_dq_" : "mtk_attn_bwd_dq_") + (wide ? "" : lay) + dt + cz;
   q.grid = (unsigned)((long long)a.q_blocks * d.B * d.H);
   q.block = wide ? 256 : 512;
   for (Launch *l : {&pre, &kv, &q}) {

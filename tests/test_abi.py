@@ -312,8 +312,13 @@ def test_attention_select_and_validation():
         with pytest.raises(mtk.MtkError) as e:
             mtk.AttentionBwdPlan(None, 1, 1, 16, 16, D)
         assert e.value.status == mtk.MTK_ERR_UNSUPPORTED
-    # D <= 128: 128-key dK/dV and 256-query dQ workgroups; D > 128: 64 keys / 64 queries per workgroup
-    assert "grids=32/4/2 " in mtk.AttentionBwdPlan(None, 1, 2, 256, 200, 64).describe() + " "
+    # D <= 128: 128-key dK/dV and 256-query dQ workgroups (laid out for 64 up to D = 64); D > 128:
+    # 64 keys / 64 queries per workgroup
+    b = mtk.AttentionBwdPlan(None, 1, 2, 256, 200, 64)
+    assert "grids=32/4/2 " in b.describe() + " " and b.describe().endswith(
+        "kernels: mtk_attn_bwd_pre_f16 mtk_attn_bwd_dkdv_d64_f16 mtk_attn_bwd_dq_d64_f16")
+    assert mtk.AttentionBwdPlan(None, 1, 2, 256, 200, 72, dtype="bf16", causal=True).describe().endswith(
+        "kernels: mtk_attn_bwd_pre_bf16 mtk_attn_bwd_dkdv_bf16_causal mtk_attn_bwd_dq_bf16_causal")
     b = mtk.AttentionBwdPlan(None, 1, 2, 256, 200, 256, causal=True)
     assert "grids=32/8/8 " in b.describe() + " " and b.describe().endswith(
         "kernels: mtk_attn_bwd_pre_f16 mtk_attn_bwd256_dkdv_f16_causal mtk_attn_bwd256_dq_f16_causal")

@@ -2,9 +2,10 @@
 headDimension: Sources/attention/Network.swift:64-107, 205-402), on the GPU through the C ABI,
 against the CPU oracle with the tolerance of tests/test_attention_bwd_gpu.py.
 
-D <= 128 (multiples of 8) runs the kernels laid out for 128 with the chunks past D loaded as zeros;
-128 < D <= 256 runs the 16-row wavefront kernels laid out for 256. Both are checked on ragged
-sequence lengths, both masks, bf16, grouped K/V heads and the config 5 shape."""
+D <= 64 (multiples of 8) runs the 32-row wavefront kernels laid out for 64, 64 < D <= 128 the
+same kernels laid out for 128, with the chunks past D loaded as zeros; 128 < D <= 256 runs the
+16-row wavefront kernels laid out for 256. All three are checked on ragged sequence lengths, both
+masks, bf16, grouped K/V heads and the config 5 shape."""
 import pytest
 
 import example_matmul_metal4_amd as mtk
@@ -13,13 +14,13 @@ from test_attention_bwd_gpu import _run_and_check
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("D", [8, 16, 64, 96, 120, 136, 160, 192, 248, 256])
+@pytest.mark.parametrize("D", [8, 16, 32, 56, 64, 72, 96, 120, 136, 160, 192, 248, 256])
 @pytest.mark.parametrize("causal", [False, True])
 def test_head_dim_sweep(dev, D, causal):
     _run_and_check(dev, 1, 2, 130, 97, causal, "f16", seed=300 + D, D=D)
 
 
-@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("D", [40, 64, 256])
 @pytest.mark.parametrize("B,H,Hkv,Sq,Skv,causal,dtype", [
     (1, 2, 2, 77, 77, True, "bf16"),
     (2, 4, 2, 200, 260, False, "f16"),   # grouped K/V heads, S_kv > S_q
@@ -39,7 +40,8 @@ def test_head_dim_config5_shape(dev, D, causal):
 
 
 def test_head_dim_plan(dev):
-    for D, kernels in ((64, ("mtk_attn_bwd_dkdv_f16", "mtk_attn_bwd_dq_f16")),
+    for D, kernels in ((64, ("mtk_attn_bwd_dkdv_d64_f16", "mtk_attn_bwd_dq_d64_f16")),
+                       (72, ("mtk_attn_bwd_dkdv_f16", "mtk_attn_bwd_dq_f16")),
                        (256, ("mtk_attn_bwd256_dkdv_f16", "mtk_attn_bwd256_dq_f16"))):
         desc = mtk.AttentionBwdPlan(dev, 1, 2, 100, 100, D=D).describe()
         assert all(k in desc for k in kernels), desc
