@@ -144,6 +144,49 @@ struct OpConv {
     r.elems = ((r.kd * a.cDZ * a.cH + r.kh * a.cDY) * a.cW + r.kw * a.cDX) * a.cC + (k0 - t * a.cC);
     return r;
   }
+  // The same decode for the channel-block-major K order (all filter taps of channels 0..63, then of
+  // 64..127, ...), walked one K-tile at a time: tap t = (kd KH + kh) KW + kw and channel block cb
+  // advance with scalar compares, where tap() takes five run-time divisions per K-tile. K-tile
+  // t C / 64 + cb of the tap-major operand order gives the same Tap.
+  struct TapWalk {
+    int kd = 0, kh = 0, kw = 0, t = 0, cb = 0;
+  };
+  __device__ __forceinline__ static void advance(const mtk_tile_args &a, TapWalk &w) {
+    ++w.t;
+    if (++w.kw == a.cKW) {
+      w.kw = 0;
+      if (++w.kh == a.cKH) {
+        w.kh = 0;
+        if (++w.kd == a.cKD) {
+          w.kd = 0;
+          w.t = 0;
+          ++w.cb;
+        }
+      }
+    }
+  }
+  // ... and for the tap-major order (all channel blocks of tap 0, then of tap 1, ...)
+  __device__ __forceinline__ static void advance_tap_major(const mtk_tile_args &a, TapWalk &w) {
+    if (++w.cb == a.cC / kBK) {
+      w.cb = 0;
+      ++w.t;
+      if (++w.kw == a.cKW) {
+        w.kw = 0;
+        if (++w.kh == a.cKH) {
+          w.kh = 0;
+          ++w.kd;
+        }
+      }
+    }
+  }
+  __device__ __forceinline__ static Tap tap_at(const mtk_tile_args &a, const TapWalk &w) {
+    Tap r;
+    r.kd = w.kd;
+    r.kh = w.kh;
+    r.kw = w.kw;
+    r.elems = ((w.kd * a.cDZ * a.cH + w.kh * a.cDY) * a.cW + w.kw * a.cDX) * a.cC + w.cb * kBK;
+    return r;
+  }
   __device__ __forceinline__ void issue(rsrc_t r, char *lds, int q, const Tap &tp) const {
     const bool ok = (pm[q] >> tp.kd) & (pm[q] >> (10 + tp.kh)) & (pm[q] >> (20 + tp.kw)) & 1u;
     lds_direct16(r, lds + (blk0 + q) * 1024, ok ? (uint32_t)(pb8[q] + tp.elems) * 2u : kOOB);
@@ -482,10 +525,27 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       for (int j = 0; j < TN; ++j) fb[S][j] = opb.frag(st + BM * 128, wave_n * WTN + j * 32, S, lane);
     };
 
+    // Convolutions (tap-major K order, kt0 = 0): the tap walk at the K-tile whose loads go out next.
+    typename std::conditional<AOP::kIsConv, typename OpConv<BM, NW>::TapWalk, int>::type walk{};
+    auto issue_walk = [&](char *st) {
+      if constexpr (AOP::kIsConv) {
+        const auto tp = OpConv<BM, NW>::tap_at(a, walk);
+#pragma unroll
+        for (int q = 0; q < PA; ++q) opa.issue(ra, st, q, tp);
+#pragma unroll
+        for (int q = 0; q < PB; ++q) opb.issue(rb, st + BM * 128, q, walk.t * (a.cC / kBK) + walk.cb);
+      }
+    };
     // Prologue: K-tiles kt0 and kt0 + 1 into the two stages, the first two k-steps' fragments.
     if (kt0 < kt1) {
-      issue_all(smem, kt0);
-      issue_all(smem + kStage, min(kt0 + 1, kt1 - 1));
+      if constexpr (AOP::kIsConv) {
+        issue_walk(smem);
+        if (kt0 + 1 < kt1) OpConv<BM, NW>::advance_tap_major(a, walk);
+        issue_walk(smem + kStage);
+      } else {
+        issue_all(smem, kt0);
+        issue_all(smem + kStage, min(kt0 + 1, kt1 - 1));
+      }
       vm_wait<PA + PB>();  // the first K-tile's loads (the second's may still be in flight)
       __builtin_amdgcn_s_barrier();
       read_step(std::integral_constant<int, 0>{}, smem);
@@ -510,9 +570,14 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       const int cur = (kt - kt0) & 1;
       char *sc = smem + cur * kStage;
       const char *sn = smem + (cur ^ 1) * kStage;
-      const int kn = min(kt + 2, kt1 - 1);
+      int kn = min(kt + 2, kt1 - 1);
       typename std::conditional<AOP::kIsConv, typename OpConv<BM, NW>::Tap, int>::type tp{};
-      if constexpr (AOP::kIsConv) tp = opa.tap(a, kn);
+      if constexpr (AOP::kIsConv) {
+        // K-tile min(kt + 2, kt1 - 1) (past the end the last one is reloaded)
+        if (kt + 2 < kt1) OpConv<BM, NW>::advance_tap_major(a, walk);
+        kn = walk.t * (a.cC / kBK) + walk.cb;
+        tp = OpConv<BM, NW>::tap_at(a, walk);
+      }
       __builtin_amdgcn_sched_barrier(0);
       static_for<0, kBK / 16>([&](auto k_c) {
         constexpr int ks = decltype(k_c)::value;
@@ -646,6 +711,8 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       cblocks = a.cC / kBK;
     }
     auto kmap = [&](int kt) { return AOP::kIsConv ? (kt % taps) * cblocks + kt / taps : kt; };
+    // convolutions: the tap walk at the K-tile whose loads go out next (kt0 = 0: no split-K)
+    typename std::conditional<AOP::kIsConv, typename OpConv<BM, NW>::TapWalk, int>::type walk{};
     constexpr int kGroups1 = (kBK / 16) * TM;
     constexpr int kLoadGroups1 = 8 < kGroups1 - TM ? 8 : kGroups1 - TM;
     constexpr int kPerGroup1 = (PA + PB + kLoadGroups1 - 1) / kLoadGroups1;
@@ -707,7 +774,17 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       }
     };
 
-    if (kt0 < kt1) issue_all(smem, kmap(kt0));
+    if constexpr (AOP::kIsConv) {
+      if (kt0 < kt1) {
+        const auto tp0 = OpConv<BM, NW>::tap_at(a, walk);
+#pragma unroll
+        for (int q = 0; q < PA; ++q) opa.issue(ra, smem, q, tp0);
+#pragma unroll
+        for (int q = 0; q < PB; ++q) opb.issue(rb, smem + BM * 128, q, walk.t * cblocks + walk.cb);
+      }
+    } else {
+      if (kt0 < kt1) issue_all(smem, kmap(kt0));
+    }
     wait_vmem();
     __syncthreads();
 #pragma unroll
@@ -726,11 +803,16 @@ __device__ __forceinline__ void tile_direct(const mtk_tile_args &a) {
       constexpr bool TAIL = decltype(tail_c)::value;
       const int cur = (kt - kt0) & 1;
       char *nxt = smem + (cur ^ 1) * kStage;
-      const int kn = kmap(min(kt + 1, kt1 - 1));
+      int kn;
       const char *sa = smem + cur * kStage;
       typename std::conditional<AOP::kIsConv, typename OpConv<BM, NW>::Tap, int>::type tp{};
       if constexpr (AOP::kIsConv) {
-        if constexpr (!TAIL) tp = opa.tap(a, kn);
+        // K-tile min(kt + 1, kt1 - 1) of the visit (past the end the last one is reloaded)
+        if (kt + 1 < kt1) OpConv<BM, NW>::advance(a, walk);
+        kn = walk.t * cblocks + walk.cb;
+        tp = OpConv<BM, NW>::tap_at(a, walk);
+      } else {
+        kn = kmap(min(kt + 1, kt1 - 1));
       }
       __builtin_amdgcn_sched_barrier(0);
       static_for<0, kLast + 1>([&](auto k_c) {
