@@ -77,6 +77,24 @@ def test_channels_and_gathers(dev, c, o):
     assert np.array_equal(y.view(np.uint16), exp.astype(np.float16).view(np.uint16))
 
 
+@pytest.mark.parametrize("rank,kd,kh,kw,o,n,hw", [(3, 2, 4, 4, 96, 1, 0), (3, 3, 3, 4, 256, 1, 0), (2, 1, 7, 7, 64, 2, 0),
+                                                  (2, 1, 5, 5, 320, 2, 0), (2, 1, 7, 7, 256, 4, 96), (2, 1, 5, 5, 256, 4, 96)])
+def test_filter_tap_counts(dev, rank, kd, kh, kw, o, n, hw):
+    # the fast gather (per-row padding masks of up to 10 taps per dimension) with filters of 32 to 49
+    # taps, bit exact on the integer generators, padding on every side; hw = 96: enough tiles for the
+    # 256x256 kernel
+    if rank == 2:
+        dims = oracle.ConvDims.conv2d(N=n, H=hw or 15, W=hw or 12, C=64, O=o, KH=kh, KW=kw, PT=kh // 2,
+                                      PB=kh - 1 - kh // 2, PL=kw // 2, PR=kw // 2)
+    else:
+        dims = oracle.ConvDims.conv3d(N=1, D=6, H=9, W=10, C=128, O=o, KD=kd, KH=kh, KW=kw, PF=1, PBk=kd - 1,
+                                      PT=1, PB=kh - 2, PL=2, PR=kw - 1)
+    assert "gather=fast" in mtk.ConvPlan(dev, mtk.conv_desc(dims, has_bias=True, rank=rank)).describe()
+    x, w, b = gen.conv3d_activation(dims), gen.conv3d_weights(dims), gen.conv3d_bias(dims)
+    y = _run(dev, dims, x, w, b, rank=rank)
+    assert _bit_exact(dims, y, x, w, b)
+
+
 @pytest.mark.parametrize("rank", [2, 3])
 def test_random_strides_dilations_padding(dev, rank):
     rng = np.random.default_rng(rank)
