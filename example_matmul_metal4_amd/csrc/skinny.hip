@@ -79,7 +79,7 @@ __device__ __forceinline__ void lds_barrier() {
 // threads) sums them for the 256 outputs of the group.
 template <int DT>
 __device__ __forceinline__ void skinny_reduce_store(const mtk_skinny_args &p, float (*red)[256], int group, int tid) {
-  for (int e = tid; e < 256; e += (int)blockDim.x) {
+  for (int e = tid; e < 256; e += 64 * p.split_k) {
     const int m = e >> 4, c = e & 15;
     const int n = group * 16 + c;
     float s = red[0][e];
@@ -100,13 +100,16 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   constexpr int kStreamPolicy = 2;
   __shared__ __attribute__((aligned(16))) float red[R][8][256];
   __shared__ __attribute__((aligned(16))) u32x4 tr[8][KS][64];  // per wavefront: 16 rows x 64 chunks
-  // the workgroup's bias values, read once before the B stream starts: a global bias load in a
-  // reduction would be the youngest vector-memory operation, and waiting for it (vmcnt(0)) would
-  // also wait for the next group's B loads in flight
-  constexpr int kBiasCache = 4096;
-  __shared__ uint16_t bias_s[kBiasCache];
+  // The workgroup's bias values, loaded into registers right after the first B group (kBiasRegs
+  // per thread, issued unconditionally: out-of-range offsets read zeros) and parked in LDS once
+  // the wait for that group covers them. A global bias load in a reduction would be the youngest
+  // vector-memory operation, and waiting for it (vmcnt(0)) would also wait for the next group's B
+  // loads in flight; loading the bias before the B stream delays the stream by a memory round trip.
+  constexpr int kBiasRegs = 8;
+  __shared__ uint16_t bias_s[kBiasRegs * 512];
 
   const int tid = threadIdx.x;
+  const int nthr = 64 * p.split_k;  // the plan launches one wavefront per K partition
   const int lane = tid & 63, w = tid >> 6;
   const int per = (p.N + (int)gridDim.x - 1) / (int)gridDim.x;
   const int c0 = (int)blockIdx.x * per, c1 = min(p.N, c0 + per);
@@ -119,17 +122,19 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   const bool k_ok = kl < k_end;
   const int r = lane & 15, q = lane >> 4;
   u32x4(&t)[KS][64] = tr[w];
-  const bool bias_cached = per <= kBiasCache;
-  if (p.has_bias && bias_cached) {
-    for (int i = tid; i < c1 - c0; i += (int)blockDim.x) bias_s[i] = ((const uint16_t *)p.bias)[c0 + i];
-  }
+  const bool bias_cached = per <= kBiasRegs * nthr;
 
+  // Row r of A or B is addressed by the scalar offset r * ld * 2 on top of the lane's fixed chunk
+  // offset (out of range past the partition); rows past the end read through a descriptor of size 0
+  // (zeros, no memory access). One address VGPR serves every load.
+  const uint32_t voff = k_ok ? (uint32_t)kl * 2u : kOOB;
+  const rsrc_t rnull = make_rsrc(p.B, 0);
   auto load_b = [&](u32x4 (&b)[KS], int col) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int n = col + s;
-      b[s] = __builtin_amdgcn_raw_buffer_load_b128(
-          rb, (k_ok && n < c1) ? (uint32_t)n * (uint32_t)p.ldb * 2u + (uint32_t)kl * 2u : kOOB, 0, kStreamPolicy);
+      b[s] = __builtin_amdgcn_raw_buffer_load_b128(n < c1 ? rb : rnull, voff, n < c1 ? (uint32_t)n * (uint32_t)p.ldb * 2u : 0u,
+                                                   kStreamPolicy);
     }
   };
 
@@ -138,8 +143,20 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   u32x4 a[KS], b0[KS], b1[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s)
-    a[s] = buf_load16(ra, (k_ok && s < p.M) ? (uint32_t)s * (uint32_t)p.lda * 2u + (uint32_t)kl * 2u : kOOB);
+    a[s] = __builtin_amdgcn_raw_buffer_load_b128(s < p.M ? ra : rnull, voff, s < p.M ? (uint32_t)s * (uint32_t)p.lda * 2u : 0u, 0);
   load_b(b0, c0);
+  uint32_t bias_r[kBiasRegs];
+  {
+    const rsrc_t rbias = make_rsrc(p.bias, (uint32_t)p.N * 2u);
+#pragma unroll
+    for (int j = 0; j < kBiasRegs; ++j) {
+      const int i = j * nthr + tid;
+      bias_r[j] = buf_load2(rbias, (p.has_bias && bias_cached && i < c1 - c0) ? (uint32_t)(c0 + i) * 2u : kOOB);
+    }
+  }
+  // keep the A transpose (which waits for A) after the first B group's and the bias's issue: the
+  // scheduler would otherwise sink those loads below it and start the B stream a round trip late
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int s = 0; s < KS; ++s) t[s][lane ^ s] = a[s];
 #pragma unroll
@@ -162,7 +179,7 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   // groups g0 .. g0 + n - 1 are parked in slots 0 .. n - 1
   auto flush = [&](int g0, int n) {
     lds_barrier();
-    for (int e = tid; e < n * 256; e += (int)blockDim.x) {
+    for (int e = tid; e < n * 256; e += nthr) {
       const int sl = e >> 8, o = e & 255, m = o >> 4;
       const int col = c0 + 16 * (g0 + sl) + (o & 15);
       float sum = red[sl][0][o];
@@ -180,6 +197,12 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   // either path and waits for the next group's loads as well, which serializes the stream.
   for (int g = 0; g < ng; g += 2) {
     load_b(b1, c0 + 16 * (g + 1));
+    if (g == 0 && bias_cached) {
+      // the first reduction's barrier orders these writes before any read
+#pragma unroll
+      for (int j = 0; j < kBiasRegs; ++j)
+        if (j * nthr < per) bias_s[j * nthr + tid] = (uint16_t)bias_r[j];
+    }
     park(g % R, mma(b0));
     if (g % R == R - 1 || g + 1 == ng) flush(g - g % R, g % R + 1);
     if (g + 1 >= ng) break;

@@ -336,8 +336,8 @@ def test_skinny_partials_shapes(dev, M, N, K, split_k, dtype):
     # many column groups per workgroup (several LDS reductions each); partitions shorter than
     # the 512 elements one load instruction covers
     (16, 60000, 256, 2, "bf16"), (4, 4097, 1024, 8, "f16"),
-    # more columns per workgroup (4297) than the kernel keeps bias values for in LDS (4096): the
-    # bias is read from global memory in the reductions
+    # more columns per workgroup (4297) than the kernel keeps bias values for in LDS (8 per
+    # thread: 512 at split-K 1): the bias is read from global memory in the reductions
     (2, 1100000, 64, 1, "f16")])
 def test_skinny_shapes(dev, M, N, K, split_k, dtype):
     A = oracle.normal(20 + M, (M, K), 0, 1, dtype)
