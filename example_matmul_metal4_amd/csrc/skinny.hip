@@ -343,15 +343,21 @@ __device__ __forceinline__ void skinny_gemm_parts(const mtk_skinny_args &p) {
   };
   load_a(a0, k0);
   load_b(b0, k0);
+  // chunk 0's loads ahead of chunk 1's: the wait at the loop head (for A of chunk j) is shared by
+  // the entry and the back edge, so the entry's issue order sets it for every iteration
+  __builtin_amdgcn_sched_barrier(0);
   load_a(a1, k0 + 32 * KS);
   load_b(b1, k0 + 32 * KS);
-  for (int j = 0; j < nch; j += 3) {
+  // whole triples in a loop without exits (a break between steps gives the loop head a second
+  // predecessor whose pending loads the compiler's waits there must also cover), then the rest
+  int j = 0;
+  for (; j + 3 <= nch; j += 3) {
     step(j, a0, b0, 0, a2, b2);
-    if (j + 1 >= nch) break;
     step(j + 1, a1, b1, 1, a0, b0);
-    if (j + 2 >= nch) break;
     step(j + 2, a2, b2, 2, a1, b1);
   }
+  if (j < nch) step(j, a0, b0, 0, a2, b2);
+  if (j + 1 < nch) step(j + 1, a1, b1, 1, a0, b0);
   wait_vmem();  // the chunks issued past the partition (zeros) land before the workgroup ends
 
   // 16x16 accumulator layout: lane (c = lane % 16, g = lane / 16), register i -> row 4g + i, col c
