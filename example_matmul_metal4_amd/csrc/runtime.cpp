@@ -217,8 +217,20 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
 
   // Decode-shaped problems (M <= 16, B [N][K]) go to the HBM-streaming skinny kernel; its
   // split-K partitions are wavefronts of one workgroup, reduced on chip with the bias fused. The
-  // grid is persistent: one workgroup per CU walking the 16-column groups.
+  // grid is persistent: one workgroup per CU walking the 16-column groups. Partitions longer than
+  // the 512 K whose A fragments stay in registers go, when K >= 2048 and there are at least two,
+  // to the partial-writing kernel below with the same partition count (16 x 4096 x 14336, split-K
+  // 8: 25 us there against 41 us on the long-partition kernel, which remains for the rest).
+  int decode_parts_split = 0;
   if (d.M <= 16 && !d.trans_a && d.trans_b && d.tile == 0 && d.K % 8 == 0 && d.lda % 8 == 0 && d.ldb % 8 == 0) {
+    int split = d.split_k == 0 ? (d.K >= 1024 ? 8 : std::max(1, d.K / 128)) : d.split_k;
+    split = std::max(1, std::min(split, 8));
+    int kps = ((d.K + split - 1) / split + 31) / 32 * 32;
+    split = (d.K + kps - 1) / kps;
+    if (kps > 512 && split >= 2 && d.K >= 2048 && d.split_mode != MTK_SPLIT_SERIAL) decode_parts_split = split;
+  }
+  if (d.M <= 16 && !decode_parts_split && !d.trans_a && d.trans_b && d.tile == 0 && d.K % 8 == 0 && d.lda % 8 == 0 &&
+      d.ldb % 8 == 0) {
     int split = d.split_k == 0 ? (d.K >= 1024 ? 8 : std::max(1, d.K / 128)) : d.split_k;
     split = std::max(1, std::min(split, 8));
     int kps = ((d.K + split - 1) / split + 31) / 32 * 32;
@@ -259,15 +271,15 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
     return MTK_OK;
   }
 
-  // 16 < M <= 32 with long K (the reference's default run, 32 x 3072 x 80000, split-K 30): B
-  // streamed once by the partial-writing skinny kernel, one workgroup per (K partition, 64
-  // columns), then the two-pass reduce. Same partition layout as the two-pass tile schedule
+  // 16 < M <= 32 with long K (the reference's default run, 32 x 3072 x 80000, split-K 30), and
+  // M <= 16 with partitions longer than 512 K (above): B streamed once by the partial-writing
+  // skinny kernel, one workgroup per (K partition, 64 columns), then the two-pass reduce. Same partition layout as the two-pass tile schedule
   // (uniform partitions of whole 64-element K-tiles); needs split_k >= 2 after the plan's choice.
-  if (d.M > 16 && d.M <= 32 && !d.trans_a && d.trans_b && d.tile == 0 && d.split_mode != MTK_SPLIT_SERIAL &&
-      d.K >= 2048 && d.K % 8 == 0 && d.lda % 8 == 0 && d.ldb % 8 == 0) {
+  if ((decode_parts_split || (d.M > 16 && d.M <= 32)) && !d.trans_a && d.trans_b && d.tile == 0 &&
+      d.split_mode != MTK_SPLIT_SERIAL && d.K >= 2048 && d.K % 8 == 0 && d.lda % 8 == 0 && d.ldb % 8 == 0) {
     const int cus = ctx ? ctx->prop.multiProcessorCount : 256;
     const long long ncb = (d.N + 63) / 64;
-    int split = d.split_k;
+    int split = decode_parts_split ? decode_parts_split : d.split_k;
     if (split == 0)  // about four workgroups per CU, partitions of at least 8 K-tiles
       split = (int)std::min<long long>(std::max<long long>(2, (4LL * cus + ncb - 1) / ncb), std::max(1, k_tiles / 8));
     split = std::min(split, k_tiles);

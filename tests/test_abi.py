@@ -160,9 +160,20 @@ def test_gemm_kernel_select_dry():
     p = mtk.GemmPlan(None, 16, 14336, 4096, dtype="bf16", has_bias=True, split_k=8)
     assert "mtk_skinny_bf16" in p.describe() and "split_k=8" in p.describe() and p.workspace_bytes == 0
     assert "mtk_skinny_f16" not in mtk.GemmPlan(None, 17, 64, 64).describe()
-    # partitions longer than 512 K reload A per pass; the grid is persistent (<= one workgroup per CU)
+    # partitions longer than 512 K: with K >= 2048 and two or more of them, the partial-writing
+    # kernel with the same partition count (one workgroup per (partition, 64 columns)) and the
+    # two-pass reduce; otherwise the long-partition kernel, which reloads A per pass on a persistent
+    # grid (<= one workgroup per CU)
     p = mtk.GemmPlan(None, 8, 14336, 8192, split_k=4)
+    assert "skinny partials M=8 N=14336 K=8192 split_k=4 k_tiles/split=32 grid=896 " in p.describe(), p.describe()
+    assert p.describe().endswith("kernels: mtk_skinny_parts_f16 mtk_splitk_reduce_f16")
+    assert p.workspace_bytes == 4 * 8 * 14336 * 4
+    p = mtk.GemmPlan(None, 8, 14336, 8192, split_k=4, split_mode="serial")
     assert "mtk_skinny_f16_long" in p.describe() and "grid=256 " in p.describe()
+    p = mtk.GemmPlan(None, 8, 14336, 1536, split_k=2)
+    assert "mtk_skinny_f16_long" in p.describe() and p.workspace_bytes == 0
+    p = mtk.GemmPlan(None, 8, 14336, 8192, split_k=1)
+    assert "mtk_skinny_f16_long" in p.describe() and p.workspace_bytes == 0
     assert "grid=3 " in mtk.GemmPlan(None, 8, 40, 256, split_k=2).describe()
     # transpose.left: A [K][M] through the transposed-read policy; never the skinny path
     p = mtk.GemmPlan(None, 4096, 4096, 4100, has_bias=True, split_k=4, trans_a=True, split_mode="two_pass")
@@ -192,7 +203,7 @@ def test_gemm_small_m_large_k_plan():
     assert "mtk_gemm_f16_nt_128x128_s" in mtk.GemmPlan(None, 32, 3072, 8192, split_k=4, split_mode="serial").describe()
     assert "skinny" not in mtk.GemmPlan(None, 32, 3072, 80000, split_k=1).describe()
     assert "skinny" not in mtk.GemmPlan(None, 32, 3072, 1024, split_k=4).describe()
-    assert "skinny partials" not in mtk.GemmPlan(None, 16, 3072, 80000, split_k=8).describe()
+    assert "skinny partials M=16 N=3072 K=80000 split_k=8 " in mtk.GemmPlan(None, 16, 3072, 80000, split_k=8).describe()
     assert "skinny" not in mtk.GemmPlan(None, 32, 3072, 8192, split_k=4, trans_a=True).describe()
     # the plan's own split: about four workgroups per CU over 48 column blocks
     d = mtk.GemmPlan(None, 24, 3072, 16384, dtype="bf16", split_k=0).describe()

@@ -314,11 +314,13 @@ def test_config3_decode_skinny_full_size(dev):
 
 @pytest.mark.parametrize("M,N,K,split_k,dtype", [
     (17, 1000, 4104, 5, "f16"), (32, 333, 2048, 2, "bf16"), (24, 4096, 16384, 0, "f16"), (32, 64, 2056, 3, "bf16"),
-    (29, 130, 70000, 30, "f16")])
+    (29, 130, 70000, 30, "f16"),
+    # M <= 16 with partitions longer than 512 K (rows M..31 of the kernel's A read zero)
+    (16, 4096, 14336, 8, "bf16"), (3, 1000, 10000, 5, "f16"), (1, 520, 2048, 2, "bf16")])
 def test_skinny_partials_shapes(dev, M, N, K, split_k, dtype):
-    # 16 < M <= 32, long K: the partial-writing skinny kernel + the two-pass reduce (partitions
-    # of whole 64-element K-tiles; the last chunk of a partition and the last partition ragged;
-    # N not a multiple of the 64-column workgroup block)
+    # 16 < M <= 32 with long K, or M <= 16 with partitions longer than 512 K: the partial-writing
+    # skinny kernel + the two-pass reduce (partitions of whole 64-element K-tiles; the last chunk
+    # of a partition and the last partition ragged; N not a multiple of the 64-column block)
     plan = mtk.GemmPlan(dev, M, N, K, dtype=dtype, has_bias=True, split_k=split_k)
     assert "skinny partials" in plan.describe(), plan.describe()
     A = oracle.normal(60 + M, (M, K), 0, 1, dtype)
