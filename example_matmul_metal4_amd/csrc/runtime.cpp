@@ -238,9 +238,13 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
     const long long groups = (d.N + 15) / 16;
     const int cus = ctx ? ctx->prop.multiProcessorCount : 256;
     Launch g;
-    // partitions of up to 512 K keep their A fragments in registers for the whole kernel
-    g.name = std::string("mtk_skinny_") + dt + (kps <= 512 ? "" : "_long");
+    // partitions of up to 512 K keep their A fragments in registers for the whole kernel; with at
+    // most four 16-column groups per workgroup and split-K >= 4 every group keeps its own LDS slot
+    // and the workgroup reduces once, at the end ("few")
     g.grid = (unsigned)std::min<long long>(groups, cus);
+    const long long per_wg = (d.N + g.grid - 1) / g.grid;
+    const bool few = kps <= 512 && split >= 4 && (per_wg + 15) / 16 <= 4;
+    g.name = std::string("mtk_skinny_") + (few ? "few_" : "") + dt + (kps <= 512 ? "" : "_long");
     g.block = (unsigned)(64 * split);
     mtk_skinny_args a{};
     a.M = d.M;

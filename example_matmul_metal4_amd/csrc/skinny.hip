@@ -36,6 +36,7 @@ namespace mtk {
 
 constexpr int kSkinnyResident = 16;  // K steps (x 32) a partition may keep resident: 512 K
 constexpr int kSkinnySlots = 2;      // column groups parked in LDS between reductions
+constexpr int kSkinnyFew = 4;        // groups per workgroup the one-reduction kernel handles
 
 template <int DT, int KS>
 struct SkinnyWave {
@@ -92,21 +93,29 @@ __device__ __forceinline__ void skinny_reduce_store(const mtk_skinny_args &p, fl
 }
 
 // Resident partitions (K per partition <= 32 * kSkinnyResident): whole-line loads transposed
-// through LDS, balanced contiguous columns, reductions every kSkinnySlots groups.
-template <int DT>
+// through LDS, balanced contiguous columns. R = kSkinnySlots: reductions every R groups, bias
+// values parked in LDS. R = kSkinnyFew (workgroups of at most R groups): every group parked in
+// its own LDS slot (160 KB with the transpose regions), one reduction at the end, each thread's
+// bias values for it held in registers.
+template <int DT, int R>
 __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
-  constexpr int KS = kSkinnyResident, R = kSkinnySlots;
+  constexpr int KS = kSkinnyResident;
+  constexpr bool kFew = R == kSkinnyFew;
+  static_assert(R == kSkinnySlots || kFew, "two slots, or one per group");
   // non-temporal B loads: each element of B is read once
   constexpr int kStreamPolicy = 2;
   __shared__ __attribute__((aligned(16))) float red[R][8][256];
   __shared__ __attribute__((aligned(16))) u32x4 tr[8][KS][64];  // per wavefront: 16 rows x 64 chunks
-  // The workgroup's bias values, loaded into registers right after the first B group (kBiasRegs
-  // per thread, issued unconditionally: out-of-range offsets read zeros) and parked in LDS once
-  // the wait for that group covers them. A global bias load in a reduction would be the youngest
-  // vector-memory operation, and waiting for it (vmcnt(0)) would also wait for the next group's B
-  // loads in flight; loading the bias before the B stream delays the stream by a memory round trip.
-  constexpr int kBiasRegs = 8;
-  __shared__ uint16_t bias_s[kBiasRegs * 512];
+  // Bias values go through registers (kBiasRegs per thread, loads issued unconditionally:
+  // out-of-range offsets read zeros). With reductions every two groups they are loaded right after
+  // the first B group and parked in LDS once the wait for that group covers them: a global bias
+  // load in a reduction would be the youngest vector-memory operation, and waiting for it
+  // (vmcnt(0)) would also wait for the next group's B loads in flight, while loading the bias
+  // before the B stream delays the stream by a memory round trip. With one reduction (at the end,
+  // when no B load is left in flight) thread t loads the values of the outputs it sums there
+  // (t, t + 64 split_k, ...) just before its barrier.
+  constexpr int kBiasRegs = kFew ? 4 : 8;  // kFew: 4 x 256 outputs over >= 256 threads (split-K >= 4)
+  __shared__ uint16_t bias_s[kFew ? 1 : kBiasRegs * 512];
 
   const int tid = threadIdx.x;
   const int nthr = 64 * p.split_k;  // the plan launches one wavefront per K partition
@@ -122,7 +131,7 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   const bool k_ok = kl < k_end;
   const int r = lane & 15, q = lane >> 4;
   u32x4(&t)[KS][64] = tr[w];
-  const bool bias_cached = per <= kBiasRegs * nthr;
+  const bool bias_cached = kFew || per <= kBiasRegs * nthr;
 
   // Row r of A or B is addressed by the scalar offset r * ld * 2 on top of the lane's fixed chunk
   // offset (out of range past the partition); rows past the end read through a descriptor of size 0
@@ -145,15 +154,18 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   for (int s = 0; s < KS; ++s)
     a[s] = __builtin_amdgcn_raw_buffer_load_b128(s < p.M ? ra : rnull, voff, s < p.M ? (uint32_t)s * (uint32_t)p.lda * 2u : 0u, 0);
   load_b(b0, c0);
-  uint32_t bias_r[kBiasRegs];
-  {
-    const rsrc_t rbias = make_rsrc(p.bias, (uint32_t)p.N * 2u);
+  const rsrc_t rbias = make_rsrc(p.bias, (uint32_t)p.N * 2u);
+  // kFew: output i of the reduction (group i / 256, column i % 16); else column c0 + i
+  auto load_bias = [&](uint32_t (&br)[kBiasRegs]) {
 #pragma unroll
     for (int j = 0; j < kBiasRegs; ++j) {
       const int i = j * nthr + tid;
-      bias_r[j] = buf_load2(rbias, (p.has_bias && bias_cached && i < c1 - c0) ? (uint32_t)(c0 + i) * 2u : kOOB);
+      const int col = kFew ? c0 + 16 * (i >> 8) + (i & 15) : c0 + i;
+      br[j] = buf_load2(rbias, (p.has_bias && bias_cached && col < c1 && (kFew || i < c1 - c0)) ? (uint32_t)col * 2u : kOOB);
     }
-  }
+  };
+  uint32_t bias_r[kBiasRegs];
+  if constexpr (!kFew) load_bias(bias_r);
   // keep the A transpose (which waits for A) after the first B group's and the bias's issue: the
   // scheduler would otherwise sink those loads below it and start the B stream a round trip late
   __builtin_amdgcn_sched_barrier(0);
@@ -178,6 +190,29 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   };
   // groups g0 .. g0 + n - 1 are parked in slots 0 .. n - 1
   auto flush = [&](int g0, int n) {
+    if constexpr (kFew) {
+      // The one reduction (g0 = 0): output e = tid + j * nthr with its bias value in bias_r[j],
+      // loaded here (the B loads are complete; held from the start, the values' registers made
+      // the compiler wait for the first B group before issuing the second) and waited for after
+      // the barrier.
+      load_bias(bias_r);
+      lds_barrier();
+#pragma unroll
+      for (int j = 0; j < kBiasRegs; ++j) {
+        const int e = tid + j * nthr;
+        if (e < n * 256) {
+          const int sl = e >> 8, o = e & 255, m = o >> 4;
+          const int col = c0 + 16 * sl + (o & 15);
+          float sum = red[sl][0][o];
+          for (int ww = 1; ww < p.split_k; ++ww) sum += red[sl][ww][o];
+          if (m < p.M && col < c1) {
+            if (p.has_bias) sum += from_bits<DT>((uint16_t)bias_r[j]);
+            ((uint16_t *)p.C)[(size_t)m * p.ldc + col] = to_bits<DT>(sum);
+          }
+        }
+      }
+      return;
+    }
     lds_barrier();
     for (int e = tid; e < n * 256; e += nthr) {
       const int sl = e >> 8, o = e & 255, m = o >> 4;
@@ -195,6 +230,22 @@ __device__ __forceinline__ void skinny_gemm_resident(const mtk_skinny_args &p) {
   // The next group's loads are issued unconditionally (columns past c1 read zeros without touching
   // memory): with a branch around them the compiler's wait before each park would have to assume
   // either path and waits for the next group's loads as well, which serializes the stream.
+  if constexpr (kFew) {
+    // ng <= R: group g parked in slot g, the reduction after the loop (no path from it back to
+    // the loop head, whose waits would otherwise have to cover its bias loads too)
+    // (scheduling barriers: each group's loads go out before the previous group's transpose)
+    for (int g = 0; g < ng; g += 2) {
+      load_b(b1, c0 + 16 * (g + 1));
+      __builtin_amdgcn_sched_barrier(0);
+      park(g, mma(b0));
+      if (g + 1 >= ng) break;
+      load_b(b0, c0 + 16 * (g + 2));
+      __builtin_amdgcn_sched_barrier(0);
+      park(g + 1, mma(b1));
+    }
+    if (ng > 0) flush(0, ng);
+    return;
+  }
   for (int g = 0; g < ng; g += 2) {
     load_b(b1, c0 + 16 * (g + 1));
     if (g == 0 && bias_cached) {
@@ -379,8 +430,13 @@ using namespace mtk;
 #define SKINNY(NAME, DT, BODY) \
   extern "C" __global__ void __launch_bounds__(512) NAME(const mtk_skinny_args a) { BODY<DT>(a); }
 
-SKINNY(mtk_skinny_f16, DT_F16, skinny_gemm_resident)
-SKINNY(mtk_skinny_bf16, DT_BF16, skinny_gemm_resident)
+#define SKINNY_RESIDENT(NAME, DT, R) \
+  extern "C" __global__ void __launch_bounds__(512) NAME(const mtk_skinny_args a) { skinny_gemm_resident<DT, R>(a); }
+
+SKINNY_RESIDENT(mtk_skinny_f16, DT_F16, kSkinnySlots)
+SKINNY_RESIDENT(mtk_skinny_bf16, DT_BF16, kSkinnySlots)
+SKINNY_RESIDENT(mtk_skinny_few_f16, DT_F16, kSkinnyFew)
+SKINNY_RESIDENT(mtk_skinny_few_bf16, DT_BF16, kSkinnyFew)
 SKINNY(mtk_skinny_f16_long, DT_F16, skinny_gemm_long)
 SKINNY(mtk_skinny_bf16_long, DT_BF16, skinny_gemm_long)
 

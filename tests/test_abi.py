@@ -44,7 +44,7 @@ def test_code_objects_hold_every_selectable_kernel():
     names += [f"mtk_gemm_{dt}_{lay}_{t}x{t}_s" for dt in ("f16", "bf16") for lay in ("nt", "nn", "tt", "tn")
               for t in (128, 256)]
     names += ["mtk_splitk_reduce_f16", "mtk_splitk_reduce_bf16", "mtk_fill_u16", "mtk_skinny_f16", "mtk_skinny_bf16",
-              "mtk_skinny_f16_long", "mtk_skinny_bf16_long"]
+              "mtk_skinny_f16_long", "mtk_skinny_bf16_long", "mtk_skinny_few_f16", "mtk_skinny_few_bf16"]
     names += [f"mtk_attn_fwd_{w}{dt}{c}" for w in ("", "pp_") for dt in ("f16", "bf16") for c in ("", "_causal")]
     names += [f"mtk_conv_f16_fast_{t}_d" for t in ("256x256", "128x128")]
     names += [f"mtk_conv_f16_gen_128x128_v{v}" for v in (8, 4, 1)]
@@ -157,8 +157,12 @@ def test_gemm_kernel_select_dry():
     p = mtk.GemmPlan(None, 512, 512, 4100, split_k=4)
     assert "split_k=4 k_tiles/split=17" in p.describe()
     # decode shapes take the HBM-streaming kernel with the K partitions reduced on chip
+    # (at most four 16-column groups per workgroup and split-K >= 4: one reduction at the end)
     p = mtk.GemmPlan(None, 16, 14336, 4096, dtype="bf16", has_bias=True, split_k=8)
-    assert "mtk_skinny_bf16" in p.describe() and "split_k=8" in p.describe() and p.workspace_bytes == 0
+    assert "mtk_skinny_few_bf16" in p.describe() and "split_k=8" in p.describe() and p.workspace_bytes == 0
+    assert "kernels: mtk_skinny_bf16" in mtk.GemmPlan(None, 16, 16400, 4096, dtype="bf16", split_k=8).describe()
+    assert "kernels: mtk_skinny_f16" in mtk.GemmPlan(None, 16, 14336, 1024, split_k=2).describe()
+    assert "kernels: mtk_skinny_few_f16" in mtk.GemmPlan(None, 16, 16384, 2048, split_k=4).describe()
     assert "mtk_skinny_f16" not in mtk.GemmPlan(None, 17, 64, 64).describe()
     # partitions longer than 512 K: with K >= 2048 and two or more of them, the partial-writing
     # kernel with the same partition count (one workgroup per (partition, 64 columns)) and the

@@ -335,6 +335,9 @@ def test_skinny_partials_shapes(dev, M, N, K, split_k, dtype):
     (16, 14336, 4096, 4, "f16"), (16, 48, 4104, 8, "f16"),
     # persistent grid: more 16-column groups than workgroups, odd and even counts per workgroup
     (5, 8211, 512, 1, "f16"), (2, 9000, 2048, 1, "bf16"),
+    # at most four groups per workgroup with split-K >= 4: one reduction (all groups in LDS);
+    # the last group ragged; just past four groups per workgroup: reductions every two groups
+    (16, 16384, 2048, 4, "bf16"), (9, 16000, 4096, 8, "f16"), (16, 16400, 4096, 8, "f16"),
     # many column groups per workgroup (several LDS reductions each); partitions shorter than
     # the 512 elements one load instruction covers
     (16, 60000, 256, 2, "bf16"), (4, 4097, 1024, 8, "f16"),
