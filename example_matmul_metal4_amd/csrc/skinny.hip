@@ -23,7 +23,9 @@
 //     current group's MFMAs (two register buffers).
 //   * Per group the partitions' fp32 16x16 results are parked in an LDS slot; every kSkinnySlots
 //     groups (and after the last) the workgroup sums partitions 0, 1, ... in order, adds the bias
-//     and stores: one barrier pair per kSkinnySlots groups instead of one barrier per group.
+//     and stores: one barrier pair per kSkinnySlots groups instead of one barrier per group. With
+//     at most kSkinnyFew groups per workgroup (and split-K >= 4) each group keeps its own slot and
+//     the workgroup reduces once, at the end (mtk_skinny_few_*).
 //   * The long kernel (longer partitions) loads fragments directly and reloads A per pass of
 //     kSkinnyResident steps (L2-resident: A is M x K).
 //   * Raw buffer loads: rows m >= M, columns n >= N and K past the partition read zero.
