@@ -58,7 +58,7 @@ def test_sweep_reaches_every_plan():
     for M, N, K, split, dtype, trans_b in CASES:
         d = mtk.GemmPlan(None, M, N, K, dtype=dtype, has_bias=True, split_k=split, trans_b=trans_b).describe()
         fams.setdefault(_family(d), []).append((M, N, K, split))
-    for want in ("mtk_skinny_few_", "mtk_skinny_parts_", "mtk_skinny_", "tile in-workgroup split-K", "tile two-pass",
+    for want in ("mtk_skinny_few_", "mtk_skinny_parts_", "_long", "mtk_skinny_", "tile in-workgroup split-K", "tile two-pass",
                  "tile one pass"):
         assert want in fams, (want, sorted(fams))
 
