@@ -24,6 +24,21 @@ def test_permute_exact(dev, shape):
     assert np.array_equal(got.view(np.uint16), exp.view(np.uint16))
 
 
+def _sweep_shapes():
+    rng = np.random.default_rng(4606)
+    return [tuple(int(v) for v in (rng.integers(1, 300), rng.integers(1, 300), rng.integers(1, 4), rng.integers(1, 6),
+                                   rng.integers(1, 6))) for _ in range(24)]
+
+
+@pytest.mark.parametrize("shape", _sweep_shapes())
+def test_permute_sweep_exact(dev, shape):
+    # seeded random O, I and filter extents (both load widths, ragged everything): bit exact
+    print(f"[permute sweep] OIDHW {shape}", flush=True)
+    w = oracle.normal(141, shape)
+    got = mtk.permute_oidhw_to_dhwio(dev, w)
+    assert np.array_equal(got.view(np.uint16), oracle.permute_oidhw_to_dhwio(w).view(np.uint16))
+
+
 def test_permute_then_conv(dev):
     # the reference's PermuteThenTensorOpSession3D: OIDHW weights re-laid out on the GPU feed the
     # conv kernel and give the DHWIO conv's result bit for bit
