@@ -58,6 +58,9 @@ def test_noalloc_skinny_partials(dev):
     # path; 30 fp32 partials of 32 x 3072 (11.8 MB) in the static scratch, then a smaller problem
     _run_both(dev, 32, 3072, 80000, 30, "auto", 60, expect="skinny partials")
     _run_both(dev, 24, 1000, 9000, 6, "auto", 70, expect="skinny partials")
+    # decode shapes (M <= 16) whose partitions are longer than 512 K take the same kernel
+    _run_both(dev, 16, 4096, 14336, 8, "auto", 80, expect="skinny partials M=16")
+    _run_both(dev, 3, 1000, 10000, 5, "auto", 90, expect="skinny partials M=3")
 
 
 def test_noalloc_config2_full_size(dev):
