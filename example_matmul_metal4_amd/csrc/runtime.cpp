@@ -318,7 +318,11 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
       ra.ldc = d.ldc;
       ra.split_k = split;
       ra.has_bias = a.has_bias;
-      ra.vec4 = (d.N % 4 == 0 && d.ldc % 4 == 0) ? 1 : 0;
+      // more than 8 partials over an output of fewer than 4 x 256 elements per CU: one output per
+      // thread, so that more workgroups keep partial loads in flight (the reference's run: 30
+      // partials of 32 x 3072, the scalar reduce ~2 us faster than four outputs per thread)
+      const bool few_outputs = split > 8 && (long long)d.M * d.N < 4LL * 256 * cus;
+      ra.vec4 = (d.N % 4 == 0 && d.ldc % 4 == 0 && !few_outputs) ? 1 : 0;
       const long long work = ra.vec4 ? (long long)d.M * d.N / 4 : (long long)d.M * d.N;
       r.grid = (unsigned)std::min<long long>((work + 255) / 256, 65535);
       set_args(r, ra);
@@ -436,7 +440,10 @@ int plan_gemm(mtk_ctx *ctx, const mtk_gemm_desc *d_in, mtk_plan **out) {
     ra.ldc = d.ldc;
     ra.split_k = split;
     ra.has_bias = a.has_bias;
-    ra.vec4 = (d.N % 4 == 0 && d.ldc % 4 == 0) ? 1 : 0;
+    // as for the partial-writing kernel: many partials over a small output, one output per thread
+    const int cus_r = ctx ? ctx->prop.multiProcessorCount : 256;
+    const bool few_outputs = split > 8 && (long long)d.M * d.N < 4LL * 256 * cus_r;
+    ra.vec4 = (d.N % 4 == 0 && d.ldc % 4 == 0 && !few_outputs) ? 1 : 0;
     const long long work = ra.vec4 ? (long long)d.M * d.N / 4 : (long long)d.M * d.N;
     r.grid = (unsigned)std::min<long long>((work + 255) / 256, 65535);
     set_args(r, ra);
